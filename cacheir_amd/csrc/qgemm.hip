@@ -1,0 +1,411 @@
+// Q4_0 / Q8_0 block weights on gfx950: tiled repack, bit-exact dequant, and the
+// dequant-fused MFMA GEMM  y[m][n] = sum_k x[m][k] * W[n][k].
+//
+// GGUF blocks (cacheir/importers/gguf.py:36,40,273-310): 32 values per block,
+// Q4_0 = fp16 d + 16 bytes (byte j: element j in the low nibble, j+16 in the
+// high nibble), value (nib - 8) * d; Q8_0 = fp16 d + 32 int8, value q * d.
+//
+// Tiled copy (made once at load, same byte count as the blocks):
+//   tile (nt, Q) = rows 16*nt..16*nt+15, columns 128*Q..128*Q+127 (4 blocks).
+//   quant bytes: 64 lanes x 16 B (Q4_0) or x 32 B (Q8_0); lane l = 16*g + r holds
+//     row 16*nt + r, columns 128*Q + 32*j + 8*g + e (j = block in quad, e = 0..7),
+//     i.e. exactly the 8-element B operand of MFMA 16x16x32 for k-step j.  Inside
+//     each dword the values sit where the fp16 conversion below picks them up.
+//   scales: 16 rows x 4 fp16 per tile.
+// A wavefront therefore loads 1 KiB (Q4_0) contiguous per instruction.
+//
+// Conversion to fp16 (no table, no int->float converts):
+//   Q4_0: (w & 0x000F000F) | 0x64006400 is the fp16 pair 1024+q; subtracting 1032
+//   gives q-8 exactly.  (w & 0x00F000F0) | 0x64006400 is 1024+16q; times 1/16 minus
+//   72 gives q-8 exactly.  w >> 8 exposes the other four nibbles the same way.
+//   Q8_0: bytes xor 0x80 are q+128; (w & 0x00FF00FF) | 0x64006400 is 1024+q+128;
+//   subtracting 1152 gives q exactly.
+//   The MFMA B operand is these exact integers; one MFMA 16x16x32 covers exactly
+//   one 32-value block, so its fp32 result is scaled by the block's d in fp32 and
+//   added to the accumulator.  Products and the scale are exact in fp32, so the
+//   only deviation from the fp32 reference (dequant then matmul, cpu.py:306-312)
+//   is fp32 summation order.
+//
+// GEMM: workgroup = 4 wavefronts on the same NT*16 output rows; the wavefronts
+// interleave over the quads of the workgroup's k-range and their fp32 accumulators
+// are summed through LDS.  grid.y splits k further (partials summed by the
+// epilogue kernels); grid.z walks 16*MT-row blocks of x.
+#include "common.hpp"
+
+namespace cir {
+namespace {
+
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t c) { return (a & m) | c; }
+
+__device__ __forceinline__ f16x2 as_h2(uint32_t v) { return __builtin_bit_cast(f16x2, v); }
+
+// 8 Q4_0 nibbles of one dword -> 8 exact fp16 integers (q - 8).
+__device__ __forceinline__ f16x8 dq_q4(uint32_t w) {
+  const f16x2 c1032 = {(f16)-1032.0f, (f16)-1032.0f};
+  const f16x2 c72 = {(f16)-72.0f, (f16)-72.0f};
+  const f16x2 s16 = {(f16)0.0625f, (f16)0.0625f};
+  const uint32_t t = w >> 8;
+  const f16x2 p0 = as_h2(and_or(w, 0x000F000Fu, 0x64006400u)) + c1032;
+  const f16x2 p1 = as_h2(and_or(w, 0x00F000F0u, 0x64006400u)) * s16 + c72;
+  const f16x2 p2 = as_h2(and_or(t, 0x000F000Fu, 0x64006400u)) + c1032;
+  const f16x2 p3 = as_h2(and_or(t, 0x00F000F0u, 0x64006400u)) * s16 + c72;
+  return f16x8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+}
+
+// 8 Q8_0 int8 values (two dwords) -> 8 exact fp16 integers q.
+__device__ __forceinline__ f16x8 dq_q8(uint32_t w0, uint32_t w1) {
+  const f16x2 c1152 = {(f16)-1152.0f, (f16)-1152.0f};
+  w0 ^= 0x80808080u;
+  w1 ^= 0x80808080u;
+  const f16x2 p0 = as_h2(and_or(w0, 0x00FF00FFu, 0x64006400u)) + c1152;
+  const f16x2 p1 = as_h2(and_or(w0 >> 8, 0x00FF00FFu, 0x64006400u)) + c1152;
+  const f16x2 p2 = as_h2(and_or(w1, 0x00FF00FFu, 0x64006400u)) + c1152;
+  const f16x2 p3 = as_h2(and_or(w1 >> 8, 0x00FF00FFu, 0x64006400u)) + c1152;
+  return f16x8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+}
+
+// Operand position e (0..7) <- Q4_0 nibble slot nu in the dword: e = 2*(nu%4) + nu/4.
+__device__ __forceinline__ int q4_elem_of_nibble(int nu) { return 2 * (nu & 3) + (nu >> 2); }
+// Operand position e <- Q8_0 byte slot beta (0..7 over the two dwords): swaps 1<->2, 5<->6.
+__device__ __forceinline__ int q8_elem_of_byte(int beta) {
+  const int lo = beta & 3;
+  const int e = (lo == 1) ? 2 : (lo == 2 ? 1 : lo);
+  return (beta & 4) + e;
+}
+
+__device__ __forceinline__ int gguf_q4_nib(const uint8_t* blk, int e) {  // element e (0..31) of a block
+  const uint8_t byte = blk[2 + (e & 15)];
+  return (e < 16) ? (byte & 15) : (byte >> 4);
+}
+
+__host__ __device__ size_t quant_bytes_per_lane(int fmt) { return fmt == CIR_Q4_0 ? 16 : 32; }
+__host__ __device__ size_t block_bytes(int fmt) { return fmt == CIR_Q4_0 ? 18 : 34; }
+
+// ---------------------------------------------------------------- repack ----
+__global__ void repack_kernel(const uint8_t* __restrict__ src, uint8_t* __restrict__ qdst, uint16_t* __restrict__ ddst,
+                              int fmt, int N, int K) {
+  const int KQ = K / 128;
+  const int NT = (N + 15) / 16;
+  const long total = (long)NT * KQ * 64;
+  const long id = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= total) return;
+  const int lane = (int)(id & 63);
+  const long tile = id >> 6;
+  const int Q = (int)(tile % KQ);
+  const int nt = (int)(tile / KQ);
+  const int r = lane & 15, g = lane >> 4;
+  const int n = nt * 16 + r;
+  const int nb = K / 32;
+  const size_t bb = block_bytes(fmt);
+  if (fmt == CIR_Q4_0) {
+    uint32_t words[4];
+    for (int j = 0; j < 4; ++j) {
+      uint32_t w = 0;
+      if (n < N) {
+        const uint8_t* blk = src + ((size_t)n * nb + 4 * Q + j) * bb;
+        for (int nu = 0; nu < 8; ++nu) w |= (uint32_t)gguf_q4_nib(blk, 8 * g + q4_elem_of_nibble(nu)) << (4 * nu);
+      }
+      words[j] = w;
+    }
+    uint32_t* out = reinterpret_cast<uint32_t*>(qdst + ((size_t)tile * 64 + lane) * 16);
+    for (int j = 0; j < 4; ++j) out[j] = words[j];
+  } else {
+    uint8_t bytes[32];
+    for (int j = 0; j < 4; ++j) {
+      const uint8_t* blk = (n < N) ? src + ((size_t)n * nb + 4 * Q + j) * bb : nullptr;
+      for (int beta = 0; beta < 8; ++beta) bytes[8 * j + beta] = blk ? blk[2 + 8 * g + q8_elem_of_byte(beta)] : 0;
+    }
+    uint8_t* out = qdst + ((size_t)tile * 64 + lane) * 32;
+    for (int i = 0; i < 32; ++i) out[i] = bytes[i];
+  }
+  if (g == 0) {
+    uint16_t* dd = ddst + ((size_t)tile * 16 + r) * 4;
+    for (int j = 0; j < 4; ++j) {
+      uint16_t dv = 0;
+      if (n < N) {
+        const uint8_t* blk = src + ((size_t)n * nb + 4 * Q + j) * bb;
+        dv = (uint16_t)(blk[0] | (blk[1] << 8));
+      }
+      dd[j] = dv;
+    }
+  }
+}
+
+// ---------------------------------------------------------------- dequant ----
+__global__ void dequant_gguf_kernel(const uint8_t* __restrict__ src, float* __restrict__ out, int fmt, int N, int K) {
+  const long nblk = (long)N * (K / 32);
+  const long b = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= nblk) return;
+  const uint8_t* blk = src + b * block_bytes(fmt);
+  const f16 dh = __builtin_bit_cast(f16, (uint16_t)(blk[0] | (blk[1] << 8)));
+  const float d = static_cast<float>(dh);
+  float* o = out + b * 32;
+  if (fmt == CIR_Q4_0) {
+    for (int e = 0; e < 32; ++e) o[e] = (float)(gguf_q4_nib(blk, e) - 8) * d;
+  } else {
+    for (int e = 0; e < 32; ++e) o[e] = (float)(int8_t)blk[2 + e] * d;
+  }
+}
+
+__global__ void dequant_tiled_kernel(const uint8_t* __restrict__ q, const uint16_t* __restrict__ dsc,
+                                     float* __restrict__ out, int fmt, int N, int K) {
+  // One thread per (tile, lane): 32 values (4 k-steps x 8).
+  const int KQ = K / 128;
+  const int NT = (N + 15) / 16;
+  const long total = (long)NT * KQ * 64;
+  const long id = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= total) return;
+  const int lane = (int)(id & 63);
+  const long tile = id >> 6;
+  const int Q = (int)(tile % KQ), nt = (int)(tile / KQ);
+  const int r = lane & 15, g = lane >> 4;
+  const int n = nt * 16 + r;
+  if (n >= N) return;
+  for (int j = 0; j < 4; ++j) {
+    const float d = static_cast<float>(__builtin_bit_cast(f16, dsc[((size_t)tile * 16 + r) * 4 + j]));
+    float* o = out + (size_t)n * K + 128 * Q + 32 * j + 8 * g;
+    if (fmt == CIR_Q4_0) {
+      const uint32_t w = reinterpret_cast<const uint32_t*>(q + ((size_t)tile * 64 + lane) * 16)[j];
+      for (int nu = 0; nu < 8; ++nu) o[q4_elem_of_nibble(nu)] = (float)((int)((w >> (4 * nu)) & 15) - 8) * d;
+    } else {
+      const uint8_t* bytes = q + ((size_t)tile * 64 + lane) * 32 + 8 * j;
+      for (int beta = 0; beta < 8; ++beta) o[q8_elem_of_byte(beta)] = (float)(int8_t)bytes[beta] * d;
+    }
+  }
+}
+
+// ------------------------------------------------------------------ GEMM -----
+// FMT: CIR_Q4_0 or CIR_Q8_0.  NT: 16-row n-tiles per wavefront.  MT: 16-row m-tiles.
+template <int FMT, int NT, int MT>
+__global__ __launch_bounds__(256) void qgemm_kernel(const f16* __restrict__ x, int ldx, const uint8_t* __restrict__ wq,
+                                                    const uint16_t* __restrict__ wd, float* __restrict__ part, int M,
+                                                    int N, int K, int quads_per_split) {
+  constexpr int LANE_BYTES = (FMT == CIR_Q4_0) ? 16 : 32;
+  __shared__ f32x4 red[3][MT * NT][64];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int li = lane & 15, lg = lane >> 4;
+  const int KQ = K / 128;
+  const int NTILES = (N + 15) / 16;
+  const int nt0 = blockIdx.x * NT;
+  const int split = blockIdx.y;
+  const int m0 = blockIdx.z * 16 * MT;
+  const int qb = split * quads_per_split;
+  const int qe = qb + quads_per_split;
+
+  f32x4 acc[MT][NT];
+#pragma unroll
+  for (int a = 0; a < MT; ++a)
+#pragma unroll
+    for (int b = 0; b < NT; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const f16* xrow[MT];
+  bool mvalid[MT];
+#pragma unroll
+  for (int a = 0; a < MT; ++a) {
+    const int m = m0 + 16 * a + li;
+    mvalid[a] = m < M;
+    xrow[a] = x + (size_t)(mvalid[a] ? m : 0) * ldx + 8 * lg;
+  }
+
+  for (int Q = qb + wave; Q < qe; Q += 4) {
+    uint4 wv[NT][LANE_BYTES / 16];
+    uint2 dv[NT];
+#pragma unroll
+    for (int b = 0; b < NT; ++b) {
+      const int ntile = min(nt0 + b, NTILES - 1);
+      const size_t tile = (size_t)ntile * KQ + Q;
+      const uint4* src = reinterpret_cast<const uint4*>(wq + (tile * 64 + lane) * LANE_BYTES);
+#pragma unroll
+      for (int c = 0; c < LANE_BYTES / 16; ++c) wv[b][c] = src[c];
+      dv[b] = reinterpret_cast<const uint2*>(wd)[tile * 16 + li];
+    }
+    f16x8 xa[MT][4];
+#pragma unroll
+    for (int a = 0; a < MT; ++a)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (mvalid[a]) {
+          xa[a][j] = *reinterpret_cast<const f16x8*>(xrow[a] + 128 * Q + 32 * j);
+        } else {
+          xa[a][j] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+        }
+      }
+#pragma unroll
+    for (int b = 0; b < NT; ++b) {
+      const float d4[4] = {static_cast<float>(__builtin_bit_cast(f16, (uint16_t)(dv[b].x & 0xFFFFu))),
+                           static_cast<float>(__builtin_bit_cast(f16, (uint16_t)(dv[b].x >> 16))),
+                           static_cast<float>(__builtin_bit_cast(f16, (uint16_t)(dv[b].y & 0xFFFFu))),
+                           static_cast<float>(__builtin_bit_cast(f16, (uint16_t)(dv[b].y >> 16)))};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        f16x8 wb;
+        if constexpr (FMT == CIR_Q4_0) {
+          const uint32_t w = (j == 0) ? wv[b][0].x : (j == 1) ? wv[b][0].y : (j == 2) ? wv[b][0].z : wv[b][0].w;
+          wb = dq_q4(w);
+        } else {
+          const uint4 v = wv[b][j >> 1];
+          const uint32_t w0 = (j & 1) ? v.z : v.x;
+          const uint32_t w1 = (j & 1) ? v.w : v.y;
+          wb = dq_q8(w0, w1);
+        }
+#pragma unroll
+        for (int a = 0; a < MT; ++a) {
+          const f32x4 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[a][j], wb, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[a][b][r] = fmaf(d4[j], c[r], acc[a][b][r]);
+        }
+      }
+    }
+  }
+
+  // Sum the four wavefronts' accumulators through LDS; wavefront 0 writes.
+  if (wave > 0) {
+#pragma unroll
+    for (int a = 0; a < MT; ++a)
+#pragma unroll
+      for (int b = 0; b < NT; ++b) red[wave - 1][a * NT + b][lane] = acc[a][b];
+  }
+  __syncthreads();
+  if (wave == 0) {
+#pragma unroll
+    for (int a = 0; a < MT; ++a)
+#pragma unroll
+      for (int b = 0; b < NT; ++b) {
+        f32x4 v = acc[a][b];
+        v += red[0][a * NT + b][lane];
+        v += red[1][a * NT + b][lane];
+        v += red[2][a * NT + b][lane];
+        const int n = (nt0 + b) * 16 + li;
+        if (nt0 + b < NTILES && n < N) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int m = m0 + 16 * a + 4 * lg + r;
+            if (m < M) part[((size_t)split * M + m) * N + n] = v[r];
+          }
+        }
+      }
+  }
+}
+
+// Dense fp32: one wavefront per output row n, lanes over k; all m rows.
+__global__ __launch_bounds__(256) void gemm_f32_kernel(const float* __restrict__ x, int ldx, const float* __restrict__ w,
+                                                       float* __restrict__ part, int M, int N, int K, int kc) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int n = blockIdx.x * 4 + wave;
+  if (n >= N) return;
+  const int split = blockIdx.y;
+  const int k0 = split * kc, k1 = min(K, k0 + kc);
+  const float* wr = w + (size_t)n * K;
+  for (int m = 0; m < M; ++m) {
+    const float* xr = x + (size_t)m * ldx;
+    float s = 0.f;
+    for (int k = k0 + lane; k < k1; k += 64) s = fmaf(xr[k], wr[k], s);
+    s = wave_sum(s);
+    if (lane == 0) part[((size_t)split * M + m) * N + n] = s;
+  }
+}
+
+template <int FMT, int NT, int MT>
+void launch_qgemm(const f16* x, int ldx, const uint8_t* wq, const uint16_t* wd, float* part, int M, int N, int K,
+                  int splits, hipStream_t s) {
+  const int NTILES = (N + 15) / 16;
+  dim3 grid((NTILES + NT - 1) / NT, splits, (M + 16 * MT - 1) / (16 * MT));
+  qgemm_kernel<FMT, NT, MT><<<grid, 256, 0, s>>>(x, ldx, wq, wd, part, M, N, K, (K / 128) / splits);
+}
+
+template <int FMT>
+void dispatch_qgemm(const f16* x, int ldx, const uint8_t* wq, const uint16_t* wd, float* part, int M, int N, int K,
+                    int splits, hipStream_t s) {
+  if (M <= 16) {
+    launch_qgemm<FMT, 4, 1>(x, ldx, wq, wd, part, M, N, K, splits, s);
+  } else {
+    launch_qgemm<FMT, 4, 2>(x, ldx, wq, wd, part, M, N, K, splits, s);
+  }
+}
+
+}  // namespace
+}  // namespace cir
+
+using namespace cir;
+
+extern "C" size_t cir_qweight_tiled_bytes(int fmt, int n, int k) {
+  if ((fmt != CIR_Q4_0 && fmt != CIR_Q8_0) || n <= 0 || k <= 0 || k % 128) return 0;
+  const size_t tiles = (size_t)((n + 15) / 16) * (k / 128);
+  return tiles * (64 * quant_bytes_per_lane(fmt) + 16 * 4 * sizeof(uint16_t));
+}
+
+extern "C" int cir_qweight_repack(const void* gguf_blocks, void* tiled, int fmt, int n, int k, void* stream) {
+  CIR_CHECK_ARG(fmt == CIR_Q4_0 || fmt == CIR_Q8_0, "repack: fmt must be CIR_Q4_0 or CIR_Q8_0 (got %d)", fmt);
+  CIR_CHECK_ARG(n >= 0 && k >= 0 && k % 128 == 0, "repack: k (%d) must be a multiple of 128", k);
+  if (n == 0 || k == 0) return 0;
+  CIR_CHECK_ARG(gguf_blocks && tiled, "repack: null pointer");
+  const size_t tiles = (size_t)((n + 15) / 16) * (k / 128);
+  uint8_t* q = static_cast<uint8_t*>(tiled);
+  uint16_t* d = reinterpret_cast<uint16_t*>(q + tiles * 64 * quant_bytes_per_lane(fmt));
+  const long threads = (long)tiles * 64;
+  repack_kernel<<<(unsigned)((threads + 255) / 256), 256, 0, as_stream(stream)>>>(static_cast<const uint8_t*>(gguf_blocks),
+                                                                                 q, d, fmt, n, k);
+  return launch_status();
+}
+
+extern "C" int cir_dequant(const void* weights, int tiled, int fmt, float* out, int n, int k, void* stream) {
+  CIR_CHECK_ARG(fmt == CIR_Q4_0 || fmt == CIR_Q8_0, "dequant: fmt must be CIR_Q4_0 or CIR_Q8_0 (got %d)", fmt);
+  CIR_CHECK_ARG(n >= 0 && k >= 0 && k % 32 == 0, "dequant: k (%d) must be a multiple of 32", k);
+  if (n == 0 || k == 0) return 0;
+  CIR_CHECK_ARG(weights && out, "dequant: null pointer");
+  hipStream_t s = as_stream(stream);
+  if (!tiled) {
+    const long nblk = (long)n * (k / 32);
+    dequant_gguf_kernel<<<(unsigned)((nblk + 255) / 256), 256, 0, s>>>(static_cast<const uint8_t*>(weights), out, fmt,
+                                                                      n, k);
+  } else {
+    CIR_CHECK_ARG(k % 128 == 0, "dequant: tiled weights need k %% 128 == 0");
+    const size_t tiles = (size_t)((n + 15) / 16) * (k / 128);
+    const uint8_t* q = static_cast<const uint8_t*>(weights);
+    const uint16_t* d = reinterpret_cast<const uint16_t*>(q + tiles * 64 * quant_bytes_per_lane(fmt));
+    const long threads = (long)tiles * 64;
+    dequant_tiled_kernel<<<(unsigned)((threads + 255) / 256), 256, 0, s>>>(q, d, out, fmt, n, k);
+  }
+  return launch_status();
+}
+
+extern "C" size_t cir_qgemm_workspace_bytes(int m, int n, int splits) {
+  if (m <= 0 || n <= 0 || splits <= 0) return 0;
+  return (size_t)splits * m * n * sizeof(float);
+}
+
+extern "C" int cir_qgemm(const void* x, int ldx, const void* w_tiled, int fmt, float* y_partial, int m, int n, int k,
+                         int splits, void* stream) {
+  CIR_CHECK_ARG(fmt == CIR_Q4_0 || fmt == CIR_Q8_0, "qgemm: fmt must be CIR_Q4_0 or CIR_Q8_0 (got %d)", fmt);
+  CIR_CHECK_ARG(m >= 0 && n >= 0 && k >= 0, "qgemm: negative size");
+  if (m == 0 || n == 0) return 0;
+  CIR_CHECK_ARG(k > 0 && k % 128 == 0, "qgemm: k (%d) must be a positive multiple of 128", k);
+  CIR_CHECK_ARG(splits >= 1 && (k / 128) % splits == 0, "qgemm: splits (%d) must divide k/128 (%d)", splits, k / 128);
+  CIR_CHECK_ARG(ldx >= k && ldx % 8 == 0, "qgemm: ldx (%d) must be >= k and a multiple of 8", ldx);
+  CIR_CHECK_ARG(x && w_tiled && y_partial, "qgemm: null pointer");
+  CIR_CHECK_ARG(splits <= 65535 && (m + 15) / 16 <= 65535, "qgemm: grid too large");
+  const size_t tiles = (size_t)((n + 15) / 16) * (k / 128);
+  const uint8_t* q = static_cast<const uint8_t*>(w_tiled);
+  const uint16_t* d = reinterpret_cast<const uint16_t*>(q + tiles * 64 * quant_bytes_per_lane(fmt));
+  const f16* xh = static_cast<const f16*>(x);
+  hipStream_t s = as_stream(stream);
+  if (fmt == CIR_Q4_0) {
+    dispatch_qgemm<CIR_Q4_0>(xh, ldx, q, d, y_partial, m, n, k, splits, s);
+  } else {
+    dispatch_qgemm<CIR_Q8_0>(xh, ldx, q, d, y_partial, m, n, k, splits, s);
+  }
+  return launch_status();
+}
+
+extern "C" int cir_gemm_f32(const float* x, int ldx, const float* w, float* y_partial, int m, int n, int k, int splits,
+                            void* stream) {
+  CIR_CHECK_ARG(m >= 0 && n >= 0 && k >= 0, "gemm_f32: negative size");
+  if (m == 0 || n == 0) return 0;
+  CIR_CHECK_ARG(k > 0 && splits >= 1 && splits <= k, "gemm_f32: bad k/splits");
+  CIR_CHECK_ARG(ldx >= k, "gemm_f32: ldx (%d) < k (%d)", ldx, k);
+  CIR_CHECK_ARG(x && w && y_partial, "gemm_f32: null pointer");
+  const int kc = (k + splits - 1) / splits;
+  dim3 grid((n + 3) / 4, splits);
+  gemm_f32_kernel<<<grid, 256, 0, as_stream(stream)>>>(x, ldx, w, y_partial, m, n, k, kc);
+  return launch_status();
+}

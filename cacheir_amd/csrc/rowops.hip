@@ -1,0 +1,303 @@
+// Row-wise kernels around the GEMMs: embedding gather, RMSNorm, residual add,
+// GEMM epilogues (split-k sum + residual / SwiGLU / RoPE + KV-page append) and
+// greedy argmax.  Reference semantics are cited at each entry point in
+// include/cacheir_hip.h.
+#include "common.hpp"
+
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+
+namespace cir {
+
+static thread_local char g_error[512] = "";
+
+void set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_error, sizeof(g_error), fmt, ap);
+  va_end(ap);
+}
+
+namespace {
+
+bool valid_dt(int dt) { return dt == CIR_F32 || dt == CIR_F16; }
+
+// ---------------------------------------------------------------- embedding --
+template <typename TT, typename TO>
+__global__ void embedding_kernel(const int64_t* __restrict__ ids, const TT* __restrict__ table, TO* __restrict__ out,
+                                 int hidden, int vocab) {
+  const int r = blockIdx.x;
+  int64_t id = ids[r];
+  // Out-of-range ids are clamped (the reference would raise IndexError on the host).
+  id = id < 0 ? 0 : (id >= vocab ? vocab - 1 : id);
+  const TT* src = table + (size_t)id * hidden;
+  TO* dst = out + (size_t)r * hidden;
+  for (int i = threadIdx.x; i < hidden; i += blockDim.x) dst[i] = from_f32<TO>(to_f32(src[i]));
+}
+
+// ---------------------------------------------------------------- rmsnorm ----
+template <typename TX, typename TW, typename TO>
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const TX* __restrict__ x, const TW* __restrict__ w,
+                                                      TO* __restrict__ out, int hidden, float eps) {
+  __shared__ float partial[4];
+  const int r = blockIdx.x;
+  const TX* xr = x + (size_t)r * hidden;
+  float ss = 0.f;
+  for (int i = threadIdx.x; i < hidden; i += 256) {
+    const float v = to_f32(xr[i]);
+    ss = fmaf(v, v, ss);
+  }
+  ss = wave_sum(ss);
+  if ((threadIdx.x & 63) == 0) partial[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  const float total = partial[0] + partial[1] + partial[2] + partial[3];
+  const float scale = 1.0f / sqrtf(total / (float)hidden + eps);
+  TO* o = out + (size_t)r * hidden;
+  for (int i = threadIdx.x; i < hidden; i += 256) o[i] = from_f32<TO>((to_f32(xr[i]) * scale) * to_f32(w[i]));
+}
+
+template <typename T>
+__global__ void add_kernel(const T* __restrict__ a, const T* __restrict__ b, T* __restrict__ out, size_t n) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) out[i] = from_f32<T>(to_f32(a[i]) + to_f32(b[i]));
+}
+
+// ---------------------------------------------------------------- epilogues --
+__device__ __forceinline__ float split_sum(const float* __restrict__ part, int splits, size_t plane, size_t idx) {
+  float v = part[idx];
+  for (int s = 1; s < splits; ++s) v += part[(size_t)s * plane + idx];
+  return v;
+}
+
+template <typename T>
+__global__ void epi_store_kernel(const float* __restrict__ part, int splits, const T* __restrict__ resid,
+                                 T* __restrict__ out, int M, int N) {
+  const size_t n_el = (size_t)M * N;
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n_el) return;
+  float v = split_sum(part, splits, n_el, i);
+  if (resid) v = to_f32(resid[i]) + v;
+  out[i] = from_f32<T>(v);
+}
+
+template <typename T>
+__global__ void epi_swiglu_kernel(const float* __restrict__ part, int splits, T* __restrict__ out, int M, int I) {
+  const size_t n_el = (size_t)M * I;
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n_el) return;
+  const int m = (int)(i / I), j = (int)(i % I);
+  const size_t plane = (size_t)M * 2 * I;
+  const float g = split_sum(part, splits, plane, (size_t)m * 2 * I + j);
+  const float u = split_sum(part, splits, plane, (size_t)m * 2 * I + I + j);
+  out[i] = from_f32<T>((g / (1.0f + expf(-g))) * u);
+}
+
+// One thread per (row, rotation pair or v element).  Columns: q [Hq*D], k [Hkv*D], v [Hkv*D].
+template <typename TQ, typename TK>
+__global__ void epi_qkv_kernel(const float* __restrict__ part, int splits, const float* __restrict__ inv_freq,
+                               const int32_t* __restrict__ positions, const int32_t* __restrict__ pt, int max_pages,
+                               TQ* __restrict__ q_out, TK* __restrict__ kp, TK* __restrict__ vp, int q_len, int Hq,
+                               int Hkv, int D, int P, int rows) {
+  const int half = D / 2;
+  const int q_pairs = Hq * half, k_pairs = Hkv * half, v_elems = Hkv * D;
+  const int per_row = q_pairs + k_pairs + v_elems;
+  const long id = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= (long)rows * per_row) return;
+  const int r = (int)(id / per_row);
+  int c = (int)(id % per_row);
+  const int b = r / q_len, s = r % q_len;
+  const int pos = positions[b] + s;
+  const int N = (Hq + 2 * Hkv) * D;
+  const size_t plane = (size_t)rows * N;
+  const float* base = part + (size_t)r * N;
+  auto col = [&](int j) { return split_sum(base, splits, plane, (size_t)j); };
+  const int page_idx = pos / P;
+  const int slot = (page_idx < max_pages) ? pt[(size_t)b * max_pages + page_idx] : -1;
+  const int off = pos - page_idx * P;
+  if (c < q_pairs + k_pairs) {
+    const bool is_q = c < q_pairs;
+    const int cc = is_q ? c : c - q_pairs;
+    const int head = cc / half, i = cc % half;
+    const int col0 = (is_q ? 0 : Hq * D) + head * D + 2 * i;
+    const float x0 = col(col0), x1 = col(col0 + 1);
+    float sn, cs;
+    sincosf((float)pos * inv_freq[i], &sn, &cs);
+    const float y0 = x0 * cs - x1 * sn;
+    const float y1 = x0 * sn + x1 * cs;
+    if (is_q) {
+      TQ* o = q_out + (size_t)r * Hq * D + head * D + 2 * i;
+      o[0] = from_f32<TQ>(y0);
+      o[1] = from_f32<TQ>(y1);
+    } else if (slot >= 0) {
+      TK* o = kp + (((size_t)slot * Hkv + head) * P + off) * D + 2 * i;
+      o[0] = from_f32<TK>(y0);
+      o[1] = from_f32<TK>(y1);
+    }
+  } else {
+    c -= q_pairs + k_pairs;
+    const int head = c / D, d = c % D;
+    const float v = col((Hq + Hkv) * D + head * D + d);
+    if (slot >= 0) vp[(((size_t)slot * Hkv + head) * P + off) * D + d] = from_f32<TK>(v);
+  }
+}
+
+// ---------------------------------------------------------------- argmax -----
+__global__ __launch_bounds__(256) void argmax_kernel(const float* __restrict__ logits, int ld, int64_t* __restrict__ ids,
+                                                     int vocab) {
+  __shared__ float sv[256];
+  __shared__ int si[256];
+  const int r = blockIdx.x;
+  const float* row = logits + (size_t)r * ld;
+  float best = -INFINITY;
+  int bi = 0x7fffffff;
+  for (int i = threadIdx.x; i < vocab; i += 256) {
+    const float v = row[i];
+    if (v > best || (v == best && i < bi)) {
+      best = v;
+      bi = i;
+    }
+  }
+  sv[threadIdx.x] = best;
+  si[threadIdx.x] = bi;
+  __syncthreads();
+  for (int stride = 128; stride > 0; stride >>= 1) {
+    if (threadIdx.x < stride) {
+      const float ov = sv[threadIdx.x + stride];
+      const int oi = si[threadIdx.x + stride];
+      if (ov > sv[threadIdx.x] || (ov == sv[threadIdx.x] && oi < si[threadIdx.x])) {
+        sv[threadIdx.x] = ov;
+        si[threadIdx.x] = oi;
+      }
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) ids[r] = si[0] == 0x7fffffff ? 0 : si[0];
+}
+
+unsigned blocks_for(size_t n, unsigned bs) { return (unsigned)((n + bs - 1) / bs); }
+
+}  // namespace
+}  // namespace cir
+
+using namespace cir;
+
+extern "C" const char* cir_version(void) { return "cacheir_amd 0.1 gfx950"; }
+extern "C" const char* cir_last_error_string(void) { return cir::g_error; }
+
+extern "C" int cir_embedding(const int64_t* ids, const void* table, int tdt, void* out, int odt, int rows, int hidden,
+                             int vocab, void* stream) {
+  CIR_CHECK_ARG(valid_dt(tdt) && valid_dt(odt), "embedding: bad dtype");
+  CIR_CHECK_ARG(rows >= 0 && hidden >= 0 && vocab > 0, "embedding: bad sizes");
+  if (rows == 0 || hidden == 0) return 0;
+  CIR_CHECK_ARG(ids && table && out, "embedding: null pointer");
+  hipStream_t s = as_stream(stream);
+  const int bs = 256;
+  if (tdt == CIR_F32 && odt == CIR_F32)
+    embedding_kernel<float, float><<<rows, bs, 0, s>>>(ids, (const float*)table, (float*)out, hidden, vocab);
+  else if (tdt == CIR_F16 && odt == CIR_F32)
+    embedding_kernel<f16, float><<<rows, bs, 0, s>>>(ids, (const f16*)table, (float*)out, hidden, vocab);
+  else if (tdt == CIR_F16 && odt == CIR_F16)
+    embedding_kernel<f16, f16><<<rows, bs, 0, s>>>(ids, (const f16*)table, (f16*)out, hidden, vocab);
+  else
+    embedding_kernel<float, f16><<<rows, bs, 0, s>>>(ids, (const float*)table, (f16*)out, hidden, vocab);
+  return launch_status();
+}
+
+extern "C" int cir_rmsnorm(const void* x, int xdt, const void* w, int wdt, void* out, int odt, int rows, int hidden,
+                           float eps, void* stream) {
+  CIR_CHECK_ARG(valid_dt(xdt) && valid_dt(wdt) && valid_dt(odt), "rmsnorm: bad dtype");
+  CIR_CHECK_ARG(rows >= 0 && hidden >= 0, "rmsnorm: bad sizes");
+  if (rows == 0 || hidden == 0) return 0;
+  CIR_CHECK_ARG(x && w && out, "rmsnorm: null pointer");
+  hipStream_t s = as_stream(stream);
+#define CIR_RMS(TX, TW, TO) \
+  rmsnorm_kernel<TX, TW, TO><<<rows, 256, 0, s>>>((const TX*)x, (const TW*)w, (TO*)out, hidden, eps)
+  const int key = xdt * 4 + wdt * 2 + odt;
+  switch (key) {
+    case 0: CIR_RMS(float, float, float); break;
+    case 1: CIR_RMS(float, float, f16); break;
+    case 2: CIR_RMS(float, f16, float); break;
+    case 3: CIR_RMS(float, f16, f16); break;
+    case 4: CIR_RMS(f16, float, float); break;
+    case 5: CIR_RMS(f16, float, f16); break;
+    case 6: CIR_RMS(f16, f16, float); break;
+    default: CIR_RMS(f16, f16, f16); break;
+  }
+#undef CIR_RMS
+  return launch_status();
+}
+
+extern "C" int cir_add(const void* a, const void* b, void* out, int dt, size_t count, void* stream) {
+  CIR_CHECK_ARG(valid_dt(dt), "add: bad dtype");
+  if (count == 0) return 0;
+  CIR_CHECK_ARG(a && b && out, "add: null pointer");
+  hipStream_t s = as_stream(stream);
+  if (dt == CIR_F32)
+    add_kernel<float><<<blocks_for(count, 256), 256, 0, s>>>((const float*)a, (const float*)b, (float*)out, count);
+  else
+    add_kernel<f16><<<blocks_for(count, 256), 256, 0, s>>>((const f16*)a, (const f16*)b, (f16*)out, count);
+  return launch_status();
+}
+
+extern "C" int cir_epilogue_store(const float* y_partial, int splits, const void* residual, void* out, int odt, int m,
+                                  int n, void* stream) {
+  CIR_CHECK_ARG(valid_dt(odt) && splits >= 1 && m >= 0 && n >= 0, "epilogue_store: bad arguments");
+  if (m == 0 || n == 0) return 0;
+  CIR_CHECK_ARG(y_partial && out, "epilogue_store: null pointer");
+  hipStream_t s = as_stream(stream);
+  const size_t ne = (size_t)m * n;
+  if (odt == CIR_F32)
+    epi_store_kernel<float><<<blocks_for(ne, 256), 256, 0, s>>>(y_partial, splits, (const float*)residual, (float*)out, m, n);
+  else
+    epi_store_kernel<f16><<<blocks_for(ne, 256), 256, 0, s>>>(y_partial, splits, (const f16*)residual, (f16*)out, m, n);
+  return launch_status();
+}
+
+extern "C" int cir_epilogue_swiglu(const float* y_partial, int splits, void* out, int odt, int m, int inter, void* stream) {
+  CIR_CHECK_ARG(valid_dt(odt) && splits >= 1 && m >= 0 && inter >= 0, "epilogue_swiglu: bad arguments");
+  if (m == 0 || inter == 0) return 0;
+  CIR_CHECK_ARG(y_partial && out, "epilogue_swiglu: null pointer");
+  hipStream_t s = as_stream(stream);
+  const size_t ne = (size_t)m * inter;
+  if (odt == CIR_F32)
+    epi_swiglu_kernel<float><<<blocks_for(ne, 256), 256, 0, s>>>(y_partial, splits, (float*)out, m, inter);
+  else
+    epi_swiglu_kernel<f16><<<blocks_for(ne, 256), 256, 0, s>>>(y_partial, splits, (f16*)out, m, inter);
+  return launch_status();
+}
+
+extern "C" int cir_epilogue_qkv_rope_append(const float* y_partial, int splits, const float* inv_freq,
+                                            const int32_t* positions, const int32_t* page_table, int max_pages,
+                                            void* q_out, int odt, void* k_pool, void* v_pool, int kvt, int batch,
+                                            int q_len, int num_heads, int num_kv_heads, int head_dim, int page_size,
+                                            void* stream) {
+  CIR_CHECK_ARG(valid_dt(odt) && valid_dt(kvt) && splits >= 1, "epilogue_qkv: bad dtype/splits");
+  CIR_CHECK_ARG(batch >= 0 && q_len >= 1 && head_dim > 0 && head_dim % 2 == 0 && num_heads > 0 && num_kv_heads > 0 &&
+                    page_size > 0 && max_pages > 0,
+                "epilogue_qkv: bad sizes");
+  if (batch == 0) return 0;
+  CIR_CHECK_ARG(y_partial && inv_freq && positions && page_table && q_out && k_pool && v_pool, "epilogue_qkv: null pointer");
+  const int rows = batch * q_len;
+  const long total = (long)rows * (num_heads * (head_dim / 2) + num_kv_heads * (head_dim / 2) + num_kv_heads * head_dim);
+  hipStream_t s = as_stream(stream);
+  const unsigned nb = (unsigned)((total + 255) / 256);
+#define CIR_QKV(TQ, TK)                                                                                            \
+  epi_qkv_kernel<TQ, TK><<<nb, 256, 0, s>>>(y_partial, splits, inv_freq, positions, page_table, max_pages, (TQ*)q_out, \
+                                            (TK*)k_pool, (TK*)v_pool, q_len, num_heads, num_kv_heads, head_dim,      \
+                                            page_size, rows)
+  if (odt == CIR_F32 && kvt == CIR_F32) CIR_QKV(float, float);
+  else if (odt == CIR_F16 && kvt == CIR_F16) CIR_QKV(f16, f16);
+  else if (odt == CIR_F32 && kvt == CIR_F16) CIR_QKV(float, f16);
+  else CIR_QKV(f16, float);
+#undef CIR_QKV
+  return launch_status();
+}
+
+extern "C" int cir_argmax(const float* logits, int ld, int64_t* ids, int rows, int vocab, void* stream) {
+  CIR_CHECK_ARG(rows >= 0 && vocab > 0 && ld >= vocab, "argmax: bad sizes");
+  if (rows == 0) return 0;
+  CIR_CHECK_ARG(logits && ids, "argmax: null pointer");
+  argmax_kernel<<<rows, 256, 0, as_stream(stream)>>>(logits, ld, ids, vocab);
+  return launch_status();
+}

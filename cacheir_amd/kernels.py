@@ -1,0 +1,263 @@
+"""Torch-tensor wrappers over the C ABI, with host-side shape/dtype/bounds checks.
+
+Every wrapper checks on the host that operand shapes, dtypes, devices and
+contiguity match what the kernel and its grid assume before anything is launched;
+violations raise ``ValueError``/``TypeError`` (mirroring the reference runtime's
+error types, ``cacheir/runtime/cuda.py:551-561``).  Page tables can additionally be
+range-checked against the pool (``check_tables=True``; costs a device sync).
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+
+from cacheir_amd import hip
+from cacheir_amd.hip import CIR_F16, CIR_F32, CIR_Q4_0, CIR_Q8_0
+
+QK = 32
+BLOCK_BYTES = {CIR_Q4_0: 18, CIR_Q8_0: 34}
+FMT_NAMES = {"q4_0": CIR_Q4_0, "q8_0": CIR_Q8_0}
+
+
+def _req(cond: bool, msg: str, exc=ValueError) -> None:
+    if not cond:
+        raise exc(msg)
+
+
+def _cuda(t: torch.Tensor, name: str) -> None:
+    _req(isinstance(t, torch.Tensor), f"{name} must be a torch.Tensor", TypeError)
+    _req(t.is_cuda, f"{name} must be on the GPU")
+    _req(t.is_contiguous(), f"{name} must be contiguous")
+
+
+# ------------------------------------------------------------------ attention --
+def attention_workspace(rows: int, num_heads: int, head_dim: int, max_context: int, device) -> torch.Tensor:
+    n = hip.size_call("cir_paged_attention_workspace_bytes", rows, num_heads, head_dim, max_context)
+    return torch.empty(max(n, 4), dtype=torch.uint8, device=device)
+
+
+def _check_pool(q, k_pool, v_pool, page_table, seq_lens, num_heads, check_tables):
+    for t, n in ((q, "q"), (k_pool, "k_pool"), (v_pool, "v_pool"), (page_table, "page_table"), (seq_lens, "seq_lens")):
+        _cuda(t, n)
+    _req(k_pool.dtype == v_pool.dtype == q.dtype, "q, k_pool and v_pool must share a dtype", TypeError)
+    _req(k_pool.dim() == 4 and v_pool.shape == k_pool.shape, "pools must be [slots, kv_heads, page_size, head_dim]")
+    _req(page_table.dtype == torch.int32 and seq_lens.dtype == torch.int32, "page_table/seq_lens must be int32", TypeError)
+    slots, kvh, psize, hd = k_pool.shape
+    _req(num_heads % kvh == 0, f"num_heads {num_heads} must be a multiple of kv heads {kvh}")
+    if check_tables and page_table.numel():
+        _req(int(page_table.min()) >= 0 and int(page_table.max()) < slots, "page_table has slots outside the pool")
+        _req(int(seq_lens.max()) <= page_table.shape[1] * psize, "seq_lens exceed the page table capacity")
+    return slots, kvh, psize, hd
+
+
+def paged_decode_attention(q, k_pool, v_pool, page_table, seq_lens, *, scale: float | None = None,
+                           out: torch.Tensor | None = None, workspace: torch.Tensor | None = None,
+                           check_tables: bool = False) -> torch.Tensor:
+    """q ``[B, Hq, D]`` -> out ``[B, Hq, D]`` over the paged context (decode, one query per sequence)."""
+    _req(q.dim() == 3, "q must be [batch, num_heads, head_dim]")
+    batch, num_heads, head_dim = q.shape
+    _, kvh, psize, hd = _check_pool(q, k_pool, v_pool, page_table, seq_lens, num_heads, check_tables)
+    _req(hd == head_dim and page_table.shape[0] == batch and seq_lens.shape == (batch,), "shape mismatch")
+    max_pages = page_table.shape[1]
+    out = torch.empty_like(q) if out is None else out
+    _cuda(out, "out")
+    _req(out.shape == q.shape and out.dtype == q.dtype, "out must match q")
+    if workspace is None:
+        workspace = attention_workspace(batch, num_heads, head_dim, max_pages * psize, q.device)
+    scale = 1.0 / math.sqrt(head_dim) if scale is None else scale
+    hip.call("cir_paged_decode_attention", q.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(), page_table.data_ptr(),
+             seq_lens.data_ptr(), out.data_ptr(), workspace.data_ptr(), workspace.numel(), batch, num_heads, kvh,
+             head_dim, psize, max_pages, float(scale), hip.dtype_code(q.dtype), hip.stream_handle())
+    return out
+
+
+def paged_prefill_attention(q, k_pool, v_pool, page_table, seq_lens, q_len: int, *, scale: float | None = None,
+                            out=None, workspace=None, check_tables: bool = False) -> torch.Tensor:
+    """q ``[B*q_len, Hq, D]``; ``seq_lens`` are lengths after appending the q_len tokens (causal)."""
+    _req(q.dim() == 3 and q_len >= 1 and q.shape[0] % q_len == 0, "q must be [batch*q_len, num_heads, head_dim]")
+    rows, num_heads, head_dim = q.shape
+    batch = rows // q_len
+    _, kvh, psize, hd = _check_pool(q, k_pool, v_pool, page_table, seq_lens, num_heads, check_tables)
+    _req(hd == head_dim and page_table.shape[0] == batch and seq_lens.shape == (batch,), "shape mismatch")
+    max_pages = page_table.shape[1]
+    out = torch.empty_like(q) if out is None else out
+    if workspace is None:
+        workspace = attention_workspace(rows, num_heads, head_dim, max_pages * psize, q.device)
+    scale = 1.0 / math.sqrt(head_dim) if scale is None else scale
+    hip.call("cir_paged_prefill_attention", q.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(), page_table.data_ptr(),
+             seq_lens.data_ptr(), out.data_ptr(), workspace.data_ptr(), workspace.numel(), batch, q_len, num_heads, kvh,
+             head_dim, psize, max_pages, float(scale), hip.dtype_code(q.dtype), hip.stream_handle())
+    return out
+
+
+# -------------------------------------------------------------- block weights --
+@dataclass
+class QWeight:
+    """A Q4_0/Q8_0 weight ``W[n, k]`` kept on the device in the tiled layout."""
+
+    tiled: torch.Tensor  # uint8
+    fmt: int
+    n: int
+    k: int
+
+    @property
+    def shape(self) -> tuple[int, int]:
+        return (self.n, self.k)
+
+    @property
+    def nbytes(self) -> int:
+        return self.tiled.numel()
+
+    @classmethod
+    def from_blocks(cls, blocks: torch.Tensor, fmt: int, n: int, k: int) -> "QWeight":
+        """Repack GGUF blocks (uint8, ``n * k/32 * block_bytes``, on the GPU) into the tiled layout."""
+        _cuda(blocks, "blocks")
+        _req(fmt in BLOCK_BYTES, f"unsupported block format {fmt}")
+        _req(k % 128 == 0, f"k={k} must be a multiple of 128 for the tiled GEMM")
+        _req(blocks.dtype == torch.uint8 and blocks.numel() == n * (k // QK) * BLOCK_BYTES[fmt],
+             "blocks must be uint8 with n*k/32*block_bytes elements")
+        size = hip.size_call("cir_qweight_tiled_bytes", fmt, n, k)
+        tiled = torch.empty(size, dtype=torch.uint8, device=blocks.device)
+        hip.call("cir_qweight_repack", blocks.data_ptr(), tiled.data_ptr(), fmt, n, k, hip.stream_handle())
+        return cls(tiled, fmt, n, k)
+
+
+def dequant_blocks(blocks: torch.Tensor, fmt: int, n: int, k: int) -> torch.Tensor:
+    _cuda(blocks, "blocks")
+    _req(blocks.numel() == n * (k // QK) * BLOCK_BYTES[fmt], "block byte count mismatch")
+    out = torch.empty((n, k), dtype=torch.float32, device=blocks.device)
+    hip.call("cir_dequant", blocks.data_ptr(), 0, fmt, out.data_ptr(), n, k, hip.stream_handle())
+    return out
+
+
+def dequant_tiled(w: QWeight) -> torch.Tensor:
+    out = torch.empty((w.n, w.k), dtype=torch.float32, device=w.tiled.device)
+    hip.call("cir_dequant", w.tiled.data_ptr(), 1, w.fmt, out.data_ptr(), w.n, w.k, hip.stream_handle())
+    return out
+
+
+def choose_splits(m: int, n: int, k: int) -> int:
+    """k-split for the tiled GEMM: enough workgroups to cover the GPU (≈ 2 per CU)."""
+    quads = k // 128
+    n_groups = (n + 63) // 64
+    m_groups = (m + 31) // 32
+    splits = 1
+    while n_groups * m_groups * splits < 512 and quads % (splits * 2) == 0 and quads // (splits * 2) >= 4:
+        splits *= 2
+    return splits
+
+
+def qgemm_partial(x: torch.Tensor, w: QWeight, splits: int | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """fp32 partials ``[splits, m, n]`` of ``x[m, k] @ W[n, k]^T`` (x fp16)."""
+    _cuda(x, "x")
+    _req(x.dtype == torch.float16, "qgemm activations must be float16", TypeError)
+    _req(x.dim() == 2 and x.shape[1] == w.k, f"x must be [m, {w.k}]")
+    m = x.shape[0]
+    splits = choose_splits(m, w.n, w.k) if splits is None else splits
+    if out is None:
+        out = torch.empty((splits, m, w.n), dtype=torch.float32, device=x.device)
+    _req(out.numel() >= splits * m * w.n and out.dtype == torch.float32, "partial buffer too small")
+    hip.call("cir_qgemm", x.data_ptr(), x.shape[1], w.tiled.data_ptr(), w.fmt, out.data_ptr(), m, w.n, w.k, splits,
+             hip.stream_handle())
+    return out.view(-1)[: splits * m * w.n].view(splits, m, w.n)
+
+
+def gemm_f32_partial(x: torch.Tensor, w: torch.Tensor, splits: int = 1, out=None) -> torch.Tensor:
+    _cuda(x, "x")
+    _cuda(w, "w")
+    _req(x.dtype == torch.float32 and w.dtype == torch.float32, "gemm_f32 needs float32 x and w", TypeError)
+    _req(x.dim() == 2 and w.dim() == 2 and x.shape[1] == w.shape[1], "x [m,k] and w [n,k] required")
+    m, k = x.shape
+    n = w.shape[0]
+    if out is None:
+        out = torch.empty((splits, m, n), dtype=torch.float32, device=x.device)
+    hip.call("cir_gemm_f32", x.data_ptr(), k, w.data_ptr(), out.data_ptr(), m, n, k, splits, hip.stream_handle())
+    return out.view(-1)[: splits * m * n].view(splits, m, n)
+
+
+# ------------------------------------------------------------------ epilogues --
+def epilogue_store(part: torch.Tensor, out_dtype: torch.dtype, residual: torch.Tensor | None = None, out=None):
+    splits, m, n = part.shape
+    if out is None:
+        out = torch.empty((m, n), dtype=out_dtype, device=part.device)
+    if residual is not None:
+        _cuda(residual, "residual")
+        _req(residual.numel() == m * n and residual.dtype == out.dtype, "residual must match the output")
+    hip.call("cir_epilogue_store", part.data_ptr(), splits, hip.ptr(residual), out.data_ptr(), hip.dtype_code(out.dtype),
+             m, n, hip.stream_handle())
+    return out
+
+
+def epilogue_swiglu(part: torch.Tensor, out_dtype: torch.dtype, out=None):
+    splits, m, n2 = part.shape
+    _req(n2 % 2 == 0, "swiglu partials need gate|up columns")
+    inter = n2 // 2
+    if out is None:
+        out = torch.empty((m, inter), dtype=out_dtype, device=part.device)
+    hip.call("cir_epilogue_swiglu", part.data_ptr(), splits, out.data_ptr(), hip.dtype_code(out.dtype), m, inter,
+             hip.stream_handle())
+    return out
+
+
+def epilogue_qkv_rope_append(part, inv_freq, positions, page_table, q_out, k_pool, v_pool, *, batch: int, q_len: int,
+                             num_heads: int, num_kv_heads: int, head_dim: int) -> torch.Tensor:
+    splits, rows, n = part.shape
+    _req(rows == batch * q_len and n == (num_heads + 2 * num_kv_heads) * head_dim, "qkv partial shape mismatch")
+    _req(positions.dtype == torch.int32 and positions.numel() == batch, "positions must be int32 [batch]")
+    _req(page_table.dtype == torch.int32 and page_table.shape[0] == batch, "page_table must be int32 [batch, pages]")
+    _req(k_pool.shape[1:] == (num_kv_heads, k_pool.shape[2], head_dim), "pool shape mismatch")
+    _req(inv_freq.numel() == head_dim // 2 and inv_freq.dtype == torch.float32, "inv_freq must be float32 [D/2]")
+    hip.call("cir_epilogue_qkv_rope_append", part.data_ptr(), splits, inv_freq.data_ptr(), positions.data_ptr(),
+             page_table.data_ptr(), page_table.shape[1], q_out.data_ptr(), hip.dtype_code(q_out.dtype),
+             k_pool.data_ptr(), v_pool.data_ptr(), hip.dtype_code(k_pool.dtype), batch, q_len, num_heads,
+             num_kv_heads, head_dim, k_pool.shape[2], hip.stream_handle())
+    return q_out
+
+
+# ---------------------------------------------------------------- row kernels --
+def embedding(ids: torch.Tensor, table: torch.Tensor, out_dtype: torch.dtype, out=None) -> torch.Tensor:
+    _cuda(ids, "ids")
+    _cuda(table, "table")
+    _req(ids.dtype == torch.int64, "ids must be int64", TypeError)
+    rows = ids.numel()
+    vocab, hidden = table.shape
+    if out is None:
+        out = torch.empty((rows, hidden), dtype=out_dtype, device=table.device)
+    hip.call("cir_embedding", ids.data_ptr(), table.data_ptr(), hip.dtype_code(table.dtype), out.data_ptr(),
+             hip.dtype_code(out.dtype), rows, hidden, vocab, hip.stream_handle())
+    return out
+
+
+def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float, out_dtype: torch.dtype, out=None) -> torch.Tensor:
+    _cuda(x, "x")
+    _cuda(w, "w")
+    hidden = x.shape[-1]
+    _req(w.numel() == hidden, "norm weight size mismatch")
+    rows = x.numel() // hidden
+    if out is None:
+        out = torch.empty(x.shape, dtype=out_dtype, device=x.device)
+    hip.call("cir_rmsnorm", x.data_ptr(), hip.dtype_code(x.dtype), w.data_ptr(), hip.dtype_code(w.dtype),
+             out.data_ptr(), hip.dtype_code(out.dtype), rows, hidden, float(eps), hip.stream_handle())
+    return out
+
+
+def add(a: torch.Tensor, b: torch.Tensor, out=None) -> torch.Tensor:
+    _cuda(a, "a")
+    _cuda(b, "b")
+    _req(a.shape == b.shape and a.dtype == b.dtype, "add operands must match")
+    out = torch.empty_like(a) if out is None else out
+    hip.call("cir_add", a.data_ptr(), b.data_ptr(), out.data_ptr(), hip.dtype_code(a.dtype), a.numel(),
+             hip.stream_handle())
+    return out
+
+
+def argmax(logits: torch.Tensor, out=None) -> torch.Tensor:
+    _cuda(logits, "logits")
+    _req(logits.dtype == torch.float32 and logits.dim() == 2, "logits must be float32 [rows, vocab]")
+    rows, vocab = logits.shape
+    if out is None:
+        out = torch.empty(rows, dtype=torch.int64, device=logits.device)
+    hip.call("cir_argmax", logits.data_ptr(), vocab, out.data_ptr(), rows, vocab, hip.stream_handle())
+    return out

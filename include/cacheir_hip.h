@@ -1,0 +1,144 @@
+/*
+ * cacheir_hip.h -- C ABI of the MI355X (gfx950) decode-step backend for CacheIR.
+ *
+ * Conventions (modelled on the reference's only C-ABI kernel boundary,
+ * cpp/src/cacheir_cuda_kernels.cu:273-411):
+ *   - every entry point returns an int status: 0 (hipSuccess) or a hipError_t
+ *     value; argument errors return hipErrorInvalidValue (1) and set the text
+ *     returned by cir_last_error_string();
+ *   - all pointers are device pointers owned by the caller; nothing is allocated
+ *     or freed inside the library; scratch memory is passed in as `workspace`
+ *     with its size from the matching *_workspace_bytes() call;
+ *   - work is enqueued asynchronously on the given stream (a hipStream_t passed as
+ *     void*; NULL = legacy default stream) and is stream-ordered;
+ *   - empty problems (batch == 0, n == 0, ...) return 0 without launching;
+ *   - the library keeps no per-call global state and is safe to call from several
+ *     host threads on different streams.
+ *
+ * Dtype codes: CIR_F32 = 0, CIR_F16 = 1.  Weight formats use GGML type ids:
+ * CIR_Q4_0 = 2, CIR_Q8_0 = 8.
+ */
+#ifndef CACHEIR_HIP_H
+#define CACHEIR_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CIR_F32 0
+#define CIR_F16 1
+#define CIR_Q4_0 2
+#define CIR_Q8_0 8
+
+/* Library identity and diagnostics. */
+const char* cir_version(void);
+const char* cir_last_error_string(void);
+
+/* ---------------------------------------------------------------- attention ---
+ * Replaces the reference's batched paged decode attention:
+ *   cacheir/backends/triton_kernels.py:174-217 (paged_attention_decode_batch_kernel),
+ *   driven by cacheir/runtime/cuda.py:1183-1253 (_try_triton_decode_attention_batch),
+ *   C-ABI analogue cpp/src/cacheir_cuda_kernels.cu:357-411.
+ * q        [batch, num_heads, head_dim]           (kv_dtype)
+ * k_pool   [slots, num_kv_heads, page_size, head_dim] (kv_dtype), v_pool likewise
+ * page_table [batch, max_pages] int32 slot ids; seq_lens [batch] int32 (tokens to
+ *   attend, the new token included); out [batch, num_heads, head_dim] (kv_dtype).
+ * Head h reads KV head h / (num_heads / num_kv_heads).  scale multiplies q.k
+ * (the reference uses 1/sqrt(head_dim)).  A sequence with seq_len 0 yields zeros.
+ * fp16 path: head_dim 128 (MFMA); fp32 path: any head_dim <= 256. */
+size_t cir_paged_attention_workspace_bytes(int rows, int num_heads, int head_dim, int max_context);
+int cir_paged_decode_attention(const void* q, const void* k_pool, const void* v_pool,
+                               const int32_t* page_table, const int32_t* seq_lens, void* out,
+                               void* workspace, size_t workspace_bytes,
+                               int batch, int num_heads, int num_kv_heads, int head_dim,
+                               int page_size, int max_pages, float scale, int kv_dtype, void* stream);
+
+/* Causal prefill over the same paged pool (reference prefill attention semantics,
+ * cacheir/runtime/cpu.py:361-368): q is [batch * q_len, num_heads, head_dim]; row
+ * (b, s) attends to tokens t < seq_lens[b] - q_len + s + 1, where seq_lens[b] is the
+ * length after the q_len new tokens were appended. */
+int cir_paged_prefill_attention(const void* q, const void* k_pool, const void* v_pool,
+                                const int32_t* page_table, const int32_t* seq_lens, void* out,
+                                void* workspace, size_t workspace_bytes,
+                                int batch, int q_len, int num_heads, int num_kv_heads, int head_dim,
+                                int page_size, int max_pages, float scale, int kv_dtype, void* stream);
+
+/* ------------------------------------------------------------ block weights ---
+ * GGUF Q4_0 / Q8_0 blocks (cacheir/importers/gguf.py:36,40,273-310) for a weight
+ * W[n, k] stored row-major, blocks along k.  The GEMM reads a tiled copy made once
+ * at load by cir_qweight_repack: nibbles/bytes regrouped into 16-row x 128-column
+ * tiles so one wavefront load is 1 KiB contiguous, and the fp16 scales in a
+ * parallel tile array.  Values are unchanged: the tiled copy dequantizes to the
+ * same (q - 8) * d (Q4_0) or q * d (Q8_0) as the GGUF blocks. */
+size_t cir_qweight_tiled_bytes(int fmt, int n, int k);
+int cir_qweight_repack(const void* gguf_blocks, void* tiled, int fmt, int n, int k, void* stream);
+
+/* Bit-exact dequantization to fp32 [n, k] from GGUF blocks (tiled = 0) or from the
+ * tiled copy (tiled = 1).  Replaces gguf.py:273-310 for device-resident weights. */
+int cir_dequant(const void* weights, int tiled, int fmt, float* out, int n, int k, void* stream);
+
+/* y_partial[split][m][n] = sum over split's k-range of x[m][k] * W[n][k]
+ * (the matmul of cacheir/runtime/cuda.py:920-954 / cpu.py:291-312).
+ * x: fp16 [m, k] row-major (row stride ldx elements); W tiled fmt blocks.
+ * Weights are dequantized to fp16 ((q-8)*d rounded once, as the reference CUDA
+ * path does by casting its fp32 dequant to fp16) and multiplied on MFMA with fp32
+ * accumulation.  splits must divide k/128.  Requires k % 128 == 0. */
+size_t cir_qgemm_workspace_bytes(int m, int n, int splits);
+int cir_qgemm(const void* x, int ldx, const void* w_tiled, int fmt, float* y_partial,
+              int m, int n, int k, int splits, void* stream);
+
+/* Dense weights W[n][k] in fp32 (x fp32) -- the fp32 parity path for unquantized
+ * artifacts.  Writes y_partial[split][m][n]; splits must divide ceil(k/256). */
+int cir_gemm_f32(const float* x, int ldx, const float* w, float* y_partial,
+                 int m, int n, int k, int splits, void* stream);
+
+/* ---------------------------------------------------------------- epilogues ---
+ * All epilogues first sum y_partial over `splits`. */
+
+/* out[m][n] = sum + (residual ? residual[m][n] : 0).  out/residual dtype odt.
+ * Residual add = graph op "add" (cpu.py:256-257) fused behind o_proj / down_proj. */
+int cir_epilogue_store(const float* y_partial, int splits, const void* residual, void* out, int odt,
+                       int m, int n, void* stream);
+
+/* SwiGLU (cpu.py:266-279): y_partial columns [0, inter) are gate, [inter, 2*inter)
+ * up; out[m][j] = silu(gate) * up, dtype odt. */
+int cir_epilogue_swiglu(const float* y_partial, int splits, void* out, int odt, int m, int inter, void* stream);
+
+/* QKV epilogue of fused_rmsnorm_qkv_rope (cpu.py:234-249, RoPE cpu.py:324-340) with
+ * the KV append of the attention node (cpu.py:352 / cuda.py:1218) fused in.
+ * y_partial columns: [0, Hq*D) q, then Hkv*D k, then Hkv*D v.  Row r = b*q_len + s
+ * is at position positions[b] + s.  Interleaved RoPE with inv_freq[D/2] (fp32,
+ * computed by the caller exactly as the reference does).  q_out [rows, Hq*D] (odt);
+ * k/v rows are written into k_pool/v_pool (kv dtype kvt) at slot
+ * page_table[b][pos / page_size], offset pos % page_size. */
+int cir_epilogue_qkv_rope_append(const float* y_partial, int splits, const float* inv_freq,
+                                 const int32_t* positions, const int32_t* page_table, int max_pages,
+                                 void* q_out, int odt, void* k_pool, void* v_pool, int kvt,
+                                 int batch, int q_len, int num_heads, int num_kv_heads, int head_dim,
+                                 int page_size, void* stream);
+
+/* ------------------------------------------------------------- row kernels ---
+ * Token embedding gather (cpu.py:223-224): out[r][:] = table[ids[r]][:]; table
+ * dtype tdt, out dtype odt; ids int64. */
+int cir_embedding(const int64_t* ids, const void* table, int tdt, void* out, int odt,
+                  int rows, int hidden, int vocab, void* stream);
+
+/* RMSNorm (cpu.py:284-289): out = (x * 1/sqrt(mean(x^2) + eps)) * w.  x dtype xdt,
+ * w dtype wdt, out dtype odt; rows of length hidden. */
+int cir_rmsnorm(const void* x, int xdt, const void* w, int wdt, void* out, int odt,
+                int rows, int hidden, float eps, void* stream);
+
+/* out = a + b elementwise (graph op "add"), all of dtype dt. */
+int cir_add(const void* a, const void* b, void* out, int dt, size_t count, void* stream);
+
+/* Greedy sampling (cpu.py:181-182, scheduler.py:535-543): ids[r] = first index of
+ * the maximum of logits[r][0:vocab] (fp32, row stride ld). */
+int cir_argmax(const float* logits, int ld, int64_t* ids, int rows, int vocab, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* CACHEIR_HIP_H */

@@ -1,0 +1,155 @@
+"""NumPy graph runtime restating CacheIR's CPU ``Runtime`` (test infrastructure only).
+
+* ``create_tiny_weights`` follows ``cacheir/importers/tiny.py:23,40-60``: one
+  ``np.random.default_rng(seed)`` stream drawn in the order embed, lm_head, then per
+  layer q, k, v, o, gate, up, down (``N(0,1)*0.02`` cast to float32); norms are ones.
+* ``OracleRuntime.run`` follows ``cacheir/runtime/cpu.py:111-140`` (graph walk over
+  nodes, env of values) with the op table of ``cpu.py:221-282``; the KV cache is the
+  contiguous per-layer cache of ``kv_cache.py:66-79``; RoPE offset is the layer's
+  length before the append (``cpu.py:314-317``).
+* ``generate_ids`` follows ``cpu.py:167-184`` on token ids (no tokenizer).
+* ``decode_batch`` runs each session's decode separately and stacks the logits,
+  which is what the reference scheduler does when it cannot batch
+  (``scheduler.py:445-454,559-565``).
+
+Weights are given as a dict ``value name -> float32 array`` (GGUF Q4_0/Q8_0 weights
+already decoded to float32 as ``gguf.py`` does at load).
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from oracle import ops
+
+
+def create_tiny_weights(*, seed: int, vocab_size: int, hidden_size: int, intermediate_size: int,
+                        num_layers: int, num_attention_heads: int, num_key_value_heads: int) -> dict[str, np.ndarray]:
+    """``tiny.py:40-60`` draw order; keys are the HF names the graph's WeightSpecs point at."""
+    rng = np.random.default_rng(seed)
+
+    def normal(shape, scale=0.02):
+        return (rng.standard_normal(shape) * scale).astype(np.float32)
+
+    w = {
+        "model.embed_tokens.weight": normal((vocab_size, hidden_size)),
+        "model.norm.weight": np.ones((hidden_size,), dtype=np.float32),
+        "lm_head.weight": normal((vocab_size, hidden_size)),
+    }
+    head_dim = hidden_size // num_attention_heads
+    kv_dim = num_key_value_heads * head_dim
+    for layer in range(num_layers):
+        p = f"model.layers.{layer}"
+        w[f"{p}.input_layernorm.weight"] = np.ones((hidden_size,), dtype=np.float32)
+        w[f"{p}.self_attn.q_proj.weight"] = normal((hidden_size, hidden_size))
+        w[f"{p}.self_attn.k_proj.weight"] = normal((kv_dim, hidden_size))
+        w[f"{p}.self_attn.v_proj.weight"] = normal((kv_dim, hidden_size))
+        w[f"{p}.self_attn.o_proj.weight"] = normal((hidden_size, hidden_size))
+        w[f"{p}.post_attention_layernorm.weight"] = np.ones((hidden_size,), dtype=np.float32)
+        w[f"{p}.mlp.gate_proj.weight"] = normal((intermediate_size, hidden_size))
+        w[f"{p}.mlp.up_proj.weight"] = normal((intermediate_size, hidden_size))
+        w[f"{p}.mlp.down_proj.weight"] = normal((hidden_size, intermediate_size))
+    return w
+
+
+class OracleRuntime:
+    """One session: a compiled-graph dict per mode, weights by HF key, and a contiguous KV cache."""
+
+    def __init__(self, graphs: dict[str, dict], weights_by_key: dict[str, np.ndarray], vocab_size: int):
+        self.graphs = graphs
+        self.vocab_size = vocab_size
+        self.keys: dict[int, np.ndarray] = {}
+        self.values: dict[int, np.ndarray] = {}
+        self.weights = {}
+        for graph in graphs.values():
+            for name, spec in graph["weights"].items():
+                self.weights[name] = np.asarray(weights_by_key[spec["key"]], dtype=np.float32)
+
+    def fork(self) -> "OracleRuntime":
+        other = OracleRuntime.__new__(OracleRuntime)
+        other.graphs, other.vocab_size, other.weights = self.graphs, self.vocab_size, self.weights
+        other.keys, other.values = {}, {}
+        return other
+
+    def kv_length(self, layer: int) -> int:
+        return int(self.keys[layer].shape[1]) if layer in self.keys else 0
+
+    def run(self, input_ids, *, mode: str = "prefill", reset_kv: bool | None = None) -> np.ndarray:
+        graph = self.graphs[mode]
+        if reset_kv is None:
+            reset_kv = mode == "prefill"
+        if mode == "prefill" and reset_kv:
+            self.keys.clear()
+            self.values.clear()
+        ids = np.asarray(input_ids, dtype=np.int64)
+        if ids.ndim == 1:
+            ids = ids[None, :]
+        env: dict[str, np.ndarray] = {"input_ids": ids}
+        env.update(self.weights)
+        for node in graph["nodes"]:
+            outs = self._execute(node, env, mode)
+            for name, value in zip(node["outputs"], outs):
+                env[name] = value
+        return env[graph["outputs"][0]]
+
+    def _append(self, layer: int, k: np.ndarray, v: np.ndarray):
+        if layer not in self.keys:
+            self.keys[layer], self.values[layer] = k.copy(), v.copy()
+        else:
+            self.keys[layer] = np.concatenate([self.keys[layer], k], axis=1)
+            self.values[layer] = np.concatenate([self.values[layer], v], axis=1)
+        return self.keys[layer], self.values[layer]
+
+    def _execute(self, node: dict, env: dict, mode: str) -> list[np.ndarray]:
+        op, ins, attrs = node["op"], node["inputs"], node["attrs"]
+        if op == "token_embedding":
+            return [env[ins[1]][env[ins[0]]]]
+        if op == "rms_norm":
+            return [ops.rms_norm(env[ins[0]], env[ins[1]], float(attrs.get("eps", 1e-6)))]
+        if op in {"matmul", "quantized_matmul"}:
+            return [ops.matmul(env[ins[0]], env[ins[1]])]
+        if op == "qkv_projection":
+            x = env[ins[0]]
+            return [ops.matmul(x, env[ins[1]]), ops.matmul(x, env[ins[2]]), ops.matmul(x, env[ins[3]])]
+        if op in {"fused_rmsnorm_qkv_rope", "quantized_fused_rmsnorm_qkv_rope"}:
+            x = ops.rms_norm(env[ins[0]], env[ins[1]], float(attrs.get("eps", 1e-6)))
+            q, k, v = ops.matmul(x, env[ins[2]]), ops.matmul(x, env[ins[3]]), ops.matmul(x, env[ins[4]])
+            off = self.kv_length(int(attrs.get("layer", 0)))
+            hd, theta = int(attrs["head_dim"]), float(attrs.get("rope_theta", 10000.0))
+            return [ops.rope_one(q, hd, theta, off), ops.rope_one(k, hd, theta, off), v]
+        if op == "rope":
+            off = self.kv_length(int(attrs.get("layer", 0)))
+            hd, theta = int(attrs["head_dim"]), float(attrs.get("rope_theta", 10000.0))
+            return [ops.rope_one(env[ins[0]], hd, theta, off), ops.rope_one(env[ins[1]], hd, theta, off)]
+        if op in {"paged_attention_prefill", "paged_attention_decode", "grouped_query_attention"}:
+            q, k, v = env[ins[0]], env[ins[1]], env[ins[2]]
+            layer = int(attrs.get("layer", 0))
+            heads, kvh, hd = int(attrs["num_heads"]), int(attrs["num_kv_heads"]), int(attrs["head_dim"])
+            b, s, _ = q.shape
+            kh, vh = self._append(layer, k.reshape(b, k.shape[1], kvh, hd), v.reshape(b, v.shape[1], kvh, hd))
+            return [ops.attention(q.reshape(b, s, heads, hd), kh, vh, heads, kvh, hd, causal=(mode == "prefill"))]
+        if op == "add":
+            return [env[ins[0]] + env[ins[1]]]
+        if op == "silu":
+            return [ops.silu(env[ins[0]])]
+        if op == "elementwise_mul":
+            return [env[ins[0]] * env[ins[1]]]
+        if op in {"fused_swiglu", "quantized_fused_swiglu"}:
+            x = env[ins[0]]
+            return [ops.silu_mul(ops.matmul(x, env[ins[1]]), ops.matmul(x, env[ins[2]]))]
+        raise NotImplementedError(f"oracle runtime does not implement op {op}")
+
+
+def generate_ids(rt: OracleRuntime, prompt_ids: list[int], max_new_tokens: int) -> tuple[list[int], np.ndarray]:
+    """``cpu.py:175-184`` on ids; returns the greedy ids and the last logits row seen."""
+    logits = rt.run([list(prompt_ids)], mode="prefill", reset_kv=True)
+    out = []
+    for _ in range(max_new_tokens):
+        nxt = int(np.argmax(logits[0, -1])) % rt.vocab_size
+        out.append(nxt)
+        logits = rt.run([[nxt]], mode="decode")
+    return out, logits
+
+
+def decode_batch(sessions: list[OracleRuntime], token_ids: list[int]) -> np.ndarray:
+    """Sequential per-session decode, stacked ``[B, 1, V]``."""
+    return np.concatenate([s.run([[int(t)]], mode="decode") for s, t in zip(sessions, token_ids)], axis=0)

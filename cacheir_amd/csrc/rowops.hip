@@ -63,6 +63,12 @@ __global__ void add_kernel(const T* __restrict__ a, const T* __restrict__ b, T* 
   if (i < n) out[i] = from_f32<T>(to_f32(a[i]) + to_f32(b[i]));
 }
 
+template <typename TI, typename TO>
+__global__ void cast_kernel(const TI* __restrict__ in, TO* __restrict__ out, size_t n) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) out[i] = from_f32<TO>(to_f32(in[i]));
+}
+
 // ---------------------------------------------------------------- epilogues --
 __device__ __forceinline__ float split_sum(const float* __restrict__ part, int splits, size_t plane, size_t idx) {
   float v = part[idx];
@@ -237,6 +243,19 @@ extern "C" int cir_add(const void* a, const void* b, void* out, int dt, size_t c
     add_kernel<float><<<blocks_for(count, 256), 256, 0, s>>>((const float*)a, (const float*)b, (float*)out, count);
   else
     add_kernel<f16><<<blocks_for(count, 256), 256, 0, s>>>((const f16*)a, (const f16*)b, (f16*)out, count);
+  return launch_status();
+}
+
+extern "C" int cir_cast(const void* in, int idt, void* out, int odt, size_t count, void* stream) {
+  CIR_CHECK_ARG(valid_dt(idt) && valid_dt(odt), "cast: bad dtype");
+  if (count == 0) return 0;
+  CIR_CHECK_ARG(in && out, "cast: null pointer");
+  hipStream_t s = as_stream(stream);
+  const unsigned nb = blocks_for(count, 256);
+  if (idt == CIR_F32 && odt == CIR_F16) cast_kernel<float, f16><<<nb, 256, 0, s>>>((const float*)in, (f16*)out, count);
+  else if (idt == CIR_F16 && odt == CIR_F32) cast_kernel<f16, float><<<nb, 256, 0, s>>>((const f16*)in, (float*)out, count);
+  else if (idt == CIR_F32) cast_kernel<float, float><<<nb, 256, 0, s>>>((const float*)in, (float*)out, count);
+  else cast_kernel<f16, f16><<<nb, 256, 0, s>>>((const f16*)in, (f16*)out, count);
   return launch_status();
 }
 

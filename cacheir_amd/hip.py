@@ -45,6 +45,7 @@ _SIGNATURES = {
     "cir_embedding": (_c_int, [_vp, _vp, _c_int, _vp, _c_int, _c_int, _c_int, _c_int, _vp]),
     "cir_rmsnorm": (_c_int, [_vp, _c_int, _vp, _c_int, _vp, _c_int, _c_int, _c_int, _c_float, _vp]),
     "cir_add": (_c_int, [_vp, _vp, _vp, _c_int, _c_size, _vp]),
+    "cir_cast": (_c_int, [_vp, _c_int, _vp, _c_int, _c_size, _vp]),
     "cir_argmax": (_c_int, [_vp, _c_int, _vp, _c_int, _c_int, _vp]),
 }
 

@@ -253,6 +253,15 @@ def add(a: torch.Tensor, b: torch.Tensor, out=None) -> torch.Tensor:
     return out
 
 
+def cast(x: torch.Tensor, dtype: torch.dtype, out=None) -> torch.Tensor:
+    _cuda(x, "x")
+    out = torch.empty(x.shape, dtype=dtype, device=x.device) if out is None else out
+    _req(out.numel() == x.numel(), "cast: size mismatch")
+    hip.call("cir_cast", x.data_ptr(), hip.dtype_code(x.dtype), out.data_ptr(), hip.dtype_code(out.dtype), x.numel(),
+             hip.stream_handle())
+    return out
+
+
 def argmax(logits: torch.Tensor, out=None) -> torch.Tensor:
     _cuda(logits, "logits")
     _req(logits.dtype == torch.float32 and logits.dim() == 2, "logits must be float32 [rows, vocab]")

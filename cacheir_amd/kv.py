@@ -1,0 +1,151 @@
+"""Device page pool and per-session paged KV caches.
+
+Contract kept from the reference (``cacheir/runtime/cuda.py:121-290,293-427``):
+* one shared allocator per runtime family (``fork()`` shares it), one pool pair
+  per layer shaped ``[slots, kv_heads, page_size, head_dim]``;
+* page tables are int32 *slot indices* into the pool, padded to
+  ``[batch, max_pages]`` (``cuda.py:1230-1234``);
+* token ``t`` lives at ``pool[slot[t // P], :, t % P, :]``.
+
+MI355X-first differences: the pools of all layers are one allocation
+``[L, slots, Hkv, P, D]`` that grows by doubling (a grow re-bases every layer at
+once); a session's slots are shared by all layers because every layer appends the
+same token positions, so one page table serves the whole step; K/V are written
+in place by the QKV epilogue kernel (no ``torch.cat`` of the whole cache and no
+page re-write, cf. ``cuda.py:322-334,172-199``).
+"""
+from __future__ import annotations
+
+import itertools
+from dataclasses import dataclass, field
+
+import torch
+
+
+class HipKVPageAllocator:
+    _owners = itertools.count(1)
+
+    def __init__(self, *, num_layers: int, kv_heads: int, head_dim: int, page_size: int = 16,
+                 dtype: torch.dtype = torch.float16, device="cuda", capacity_pages: int = 64,
+                 max_resident_pages: int | None = None):
+        self.num_layers, self.kv_heads, self.head_dim = num_layers, kv_heads, head_dim
+        self.page_size = max(1, int(page_size))
+        self.dtype = dtype
+        self.device = torch.device(device)
+        self.max_resident_pages = max_resident_pages
+        self.capacity = 0
+        self.k = self.v = None
+        self._free: list[int] = []
+        self._owner_of: dict[int, str] = {}
+        self.pool_grows = 0
+        self.allocated_pages_total = 0
+        self.released_pages = 0
+        self.generation = 0  # bumps when the pool tensors are re-allocated
+        self._grow(max(1, int(capacity_pages)))
+
+    def _grow(self, capacity: int) -> None:
+        shape = (self.num_layers, capacity, self.kv_heads, self.page_size, self.head_dim)
+        k = torch.zeros(shape, dtype=self.dtype, device=self.device)
+        v = torch.zeros(shape, dtype=self.dtype, device=self.device)
+        if self.k is not None:
+            k[:, : self.capacity] = self.k
+            v[:, : self.capacity] = self.v
+        self._free.extend(range(capacity - 1, self.capacity - 1, -1))
+        self.k, self.v, self.capacity = k, v, capacity
+        self.pool_grows += 1
+        self.generation += 1
+
+    def reserve(self, pages: int) -> None:
+        """Grow once so that ``pages`` more slots can be allocated without re-basing."""
+        if len(self._free) < pages:
+            self._grow(max(self.capacity * 2, self.capacity + pages - len(self._free)))
+
+    def new_owner(self) -> str:
+        return f"hip-session-{next(self._owners)}"
+
+    def allocate(self, owner: str) -> int:
+        if self.max_resident_pages is not None and len(self._owner_of) >= self.max_resident_pages:
+            raise RuntimeError(f"KV page budget exhausted ({self.max_resident_pages} resident pages)")
+        if not self._free:
+            self._grow(self.capacity * 2)
+        slot = self._free.pop()
+        self._owner_of[slot] = owner
+        self.allocated_pages_total += 1
+        return slot
+
+    def release(self, slots: list[int]) -> None:
+        for s in slots:
+            if self._owner_of.pop(s, None) is not None:
+                self._free.append(s)
+                self.released_pages += 1
+
+    def layer_pools(self, layer: int) -> tuple[torch.Tensor, torch.Tensor]:
+        return self.k[layer], self.v[layer]
+
+    @property
+    def page_bytes(self) -> int:
+        return 2 * self.kv_heads * self.page_size * self.head_dim * self.k.element_size()
+
+    def stats(self) -> dict[str, object]:
+        return {
+            "page_size": self.page_size,
+            "page_bytes": self.page_bytes,
+            "allocated_pages_total": self.allocated_pages_total,
+            "resident_pages": len(self._owner_of),
+            "released_pages": self.released_pages,
+            "max_resident_pages": self.max_resident_pages,
+            "pool_grows": self.pool_grows,
+            "persistent_pools": [{
+                "layers": self.num_layers, "device": str(self.device), "dtype": str(self.dtype),
+                "kv_heads": self.kv_heads, "head_dim": self.head_dim, "slots": len(self._owner_of),
+                "capacity": self.capacity,
+                "bytes": int(self.k.numel() * self.k.element_size() * 2),
+            }],
+        }
+
+
+@dataclass
+class HipPagedKVCache:
+    """One session's pages: slot list shared by all layers, and the token count."""
+
+    allocator: HipKVPageAllocator
+    owner: str = ""
+    slots: list[int] = field(default_factory=list)
+    tokens: int = 0
+
+    def __post_init__(self):
+        if not self.owner:
+            self.owner = self.allocator.new_owner()
+
+    @property
+    def page_size(self) -> int:
+        return self.allocator.page_size
+
+    def __contains__(self, layer: int) -> bool:
+        return self.tokens > 0 and 0 <= layer < self.allocator.num_layers
+
+    def length(self, layer: int = 0) -> int:
+        return self.tokens if layer in self else 0
+
+    def ensure_capacity(self, total_tokens: int) -> None:
+        need = -(-total_tokens // self.page_size)
+        while len(self.slots) < need:
+            self.slots.append(self.allocator.allocate(self.owner))
+
+    def clear(self) -> None:
+        self.allocator.release(self.slots)
+        self.slots = []
+        self.tokens = 0
+
+    def pages(self) -> list[dict[str, int]]:
+        p = self.page_size
+        return [{"page_id": s, "start": i * p, "length": min(p, self.tokens - i * p)}
+                for i, s in enumerate(self.slots) if i * p < self.tokens]
+
+    def stats(self) -> dict[str, object]:
+        return {
+            "page_size": self.page_size,
+            "layers": {str(l): {"tokens": self.tokens, "pages": self.pages()} for l in range(self.allocator.num_layers)}
+            if self.tokens else {},
+            "allocator": self.allocator.stats(),
+        }

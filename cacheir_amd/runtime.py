@@ -1,0 +1,566 @@
+"""``HipRuntime``: the ROCm backend's artifact runtime for CacheIR decode graphs.
+
+Duck-typed to the reference ``CudaRuntime`` (``cacheir/runtime/cuda.py:430-1263``)
+so the scheduler, benchmark and server can drive it unchanged:
+``run(input_ids, mode=, reset_kv=)``, ``run_decode_batch(sessions, token_ids)``,
+``run_prefill_batch(sessions, batches)``, ``prefill_tokens``, ``generate``,
+``generate_ids``, ``fork()``, ``synchronize()``, ``cache_stats()`` and the
+attributes ``artifact, tokenizer, prefix_cache, kv_cache, kv_allocator,
+supports_variable_prefill_batch``.  Error types follow the reference
+(``ValueError`` / ``TypeError`` / ``NotImplementedError`` / ``RuntimeError``,
+``cuda.py:551-561,777,531-536``).
+
+Execution: each (mode, batch, tokens-per-sequence, page-table width) gets a
+``StepPlan`` -- the lowered graph translated once into a list of C-ABI launches
+over static device buffers.  The host only fills the token ids, positions and page
+table per step; a plan can be captured into a HIP graph and replayed
+(``cacheir/backends/cuda_graphs.py:38-55`` names exactly these static inputs).
+Fusions done at plan time (semantics unchanged):
+* ``fused_rmsnorm_qkv_rope``: RMSNorm -> one GEMM over Q|K|V -> epilogue that
+  applies interleaved RoPE at the pre-append position and writes K/V straight into
+  the page pool, i.e. the append the attention node would do (``cpu.py:239-241,352``);
+* ``matmul`` whose only consumer is a residual ``add``: the add runs in the GEMM
+  epilogue;
+* ``fused_swiglu``: one GEMM over gate|up, SiLU-mul in the epilogue.
+There is no CPU fallback anywhere on this path.
+"""
+from __future__ import annotations
+
+import itertools
+import json
+from collections import OrderedDict
+from pathlib import Path
+from typing import Any, Iterable
+
+import numpy as np
+import torch
+
+from cacheir_amd import hip, kernels
+from cacheir_amd.artifact import CompileArtifact
+from cacheir_amd.ir import Graph, Node
+from cacheir_amd.kv import HipKVPageAllocator, HipPagedKVCache
+from cacheir_amd.weights import GGUFSource, HipWeightStore, NpzDir, SyntheticQuant
+
+_QKV_OPS = {"fused_rmsnorm_qkv_rope", "quantized_fused_rmsnorm_qkv_rope"}
+_SWIGLU_OPS = {"fused_swiglu", "quantized_fused_swiglu"}
+_MATMUL_OPS = {"matmul", "quantized_matmul"}
+_ATTN_OPS = {"paged_attention_decode", "paged_attention_prefill", "grouped_query_attention"}
+_GGUF_KEYS = {"model.embed_tokens.weight": "token_embd.weight", "model.norm.weight": "output_norm.weight",
+              "lm_head.weight": "output.weight"}
+_GGUF_LAYER_KEYS = {"input_layernorm.weight": "attn_norm.weight", "self_attn.q_proj.weight": "attn_q.weight",
+                    "self_attn.k_proj.weight": "attn_k.weight", "self_attn.v_proj.weight": "attn_v.weight",
+                    "self_attn.o_proj.weight": "attn_output.weight",
+                    "post_attention_layernorm.weight": "ffn_norm.weight", "mlp.gate_proj.weight": "ffn_gate.weight",
+                    "mlp.up_proj.weight": "ffn_up.weight", "mlp.down_proj.weight": "ffn_down.weight"}
+
+
+def hip_runtime_available() -> bool:
+    return bool(torch.cuda.is_available() and hip.LIB_PATH.exists())
+
+
+def gguf_key_map(num_layers: int) -> dict[str, str]:
+    """HF weight names -> GGUF tensor names (the mapping of ``cacheir/compiler.py:85-107``)."""
+    m = dict(_GGUF_KEYS)
+    for layer in range(num_layers):
+        for hf, gg in _GGUF_LAYER_KEYS.items():
+            m[f"model.layers.{layer}.{hf}"] = f"blk.{layer}.{gg}"
+    return m
+
+
+def rope_inv_freq(head_dim: int, theta: float) -> np.ndarray:
+    """``1 / theta ** (arange(0, D/2, float32) * 2 / D)`` evaluated in float32 as ``cpu.py:330`` does."""
+    return (1.0 / (theta ** (np.arange(0, head_dim // 2, dtype=np.float32) * 2.0 / head_dim))).astype(np.float32)
+
+
+class ByteTokenizer:
+    """Byte tokenizer with the reference's encode/decode rules (``cacheir/runtime/tokenizer.py:7-23``)."""
+
+    def __init__(self, vocab_size: int):
+        self.vocab_size = max(1, int(vocab_size))
+
+    def encode(self, text: str) -> list[int]:
+        if not isinstance(text, str):
+            raise TypeError("encode expects a string prompt")
+        return [b % self.vocab_size for b in (text.encode("utf-8") or b"\x00")]
+
+    def decode(self, ids: Iterable[int]) -> str:
+        return "".join(chr(v) if 32 <= v <= 126 else f"<{v}>" for v in (int(i) % self.vocab_size for i in ids))
+
+
+class PrefixCache:
+    """LRU map ``token prefix -> page snapshot`` (``cacheir/runtime/kv_cache.py:262-307``).
+
+    A snapshot holds device copies of the prefix's pages for every layer, so a hit
+    restores the KV of a prompt without recomputing it."""
+
+    def __init__(self, capacity: int = 8):
+        self.capacity = max(1, int(capacity))
+        self._entries: OrderedDict[tuple[int, ...], Any] = OrderedDict()
+        self.hits = self.misses = self.evictions = 0
+
+    def put(self, token_ids, snapshot) -> None:
+        key = tuple(int(t) for t in token_ids)
+        self._entries.pop(key, None)
+        self._entries[key] = snapshot
+        while len(self._entries) > self.capacity:
+            self._entries.popitem(last=False)
+            self.evictions += 1
+
+    def longest_prefix(self, token_ids):
+        query = tuple(int(t) for t in token_ids)
+        best, value = (), None
+        for key, snap in self._entries.items():
+            if len(key) > len(best) and query[: len(key)] == key:
+                best, value = key, snap
+        if value is not None:
+            self._entries.move_to_end(best)
+            self.hits += 1
+        else:
+            self.misses += 1
+        return best, value
+
+    def stats(self) -> dict[str, int]:
+        return {"capacity": self.capacity, "entries": len(self._entries), "hits": self.hits, "misses": self.misses,
+                "evictions": self.evictions}
+
+
+# ============================================================================ plan ==
+class StepPlan:
+    """One graph translated into C-ABI launches over static buffers."""
+
+    def __init__(self, rt: "HipRuntime", mode: str, batch: int, q_len: int, max_pages: int):
+        self.rt, self.mode, self.batch, self.q_len, self.max_pages = rt, mode, batch, q_len, max_pages
+        self.generation = rt.kv_allocator.generation
+        dev = rt.device
+        self.rows = rows = batch * q_len
+        self.ids = torch.zeros(rows, dtype=torch.int64, device=dev)
+        self.positions = torch.zeros(batch, dtype=torch.int32, device=dev)
+        self.seq_lens = torch.zeros(batch, dtype=torch.int32, device=dev)
+        self.page_table = torch.zeros((batch, max_pages), dtype=torch.int32, device=dev)
+        self.launches: list = []
+        self.graph_obj: torch.cuda.CUDAGraph | None = None
+        self._gemm_need = 1
+        self._build(rt.artifact.graph(mode))
+        self.gemm_ws = torch.empty(self._gemm_need, dtype=torch.float32, device=dev)
+        attn_need = kernels.hip.size_call("cir_paged_attention_workspace_bytes", rows, rt.config.num_attention_heads,
+                                          rt.config.head_dim, max_pages * rt.kv_allocator.page_size)
+        self.attn_ws = torch.empty(max(attn_need, 4), dtype=torch.uint8, device=dev)
+
+    # ------------------------------------------------------------------ build --
+    def _build(self, graph: Graph) -> None:
+        rt, rows = self.rt, self.rows
+        consumers = graph.consumers()
+        env: dict[str, Any] = {}
+        skip: set[int] = set()
+        appended: set[int] = set()
+        self.logits_name = graph.outputs[0]
+
+        def gemm_dtype(weight) -> torch.dtype:
+            return torch.float16 if isinstance(weight, kernels.QWeight) else torch.float32
+
+        def input_dtype_for(value: str) -> torch.dtype | None:
+            """The dtype the first matmul-family consumer of ``value`` wants, if any."""
+            for c in consumers.get(value, []):
+                if c.op in _MATMUL_OPS:
+                    return gemm_dtype(rt.weights.matmul_weight((c.inputs[1],)))
+                if c.op in _SWIGLU_OPS:
+                    return gemm_dtype(rt.weights.matmul_weight((c.inputs[1], c.inputs[2])))
+            return None
+
+        def buf(n: int, dtype: torch.dtype) -> torch.Tensor:
+            return torch.empty((rows, n), dtype=dtype, device=rt.device)
+
+        def as_dtype(t: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+            if t.dtype == dtype:
+                return t
+            out = torch.empty(t.shape, dtype=dtype, device=t.device)
+            self.launches.append(lambda t=t, out=out: kernels.cast(t, out.dtype, out=out))
+            return out
+
+        def gemm(x: torch.Tensor, weight) -> tuple[Any, int, int]:
+            """Queue the GEMM into the shared workspace; returns (partials getter, splits, n)."""
+            if isinstance(weight, kernels.QWeight):
+                n, k = weight.n, weight.k
+                splits = kernels.choose_splits(rows, n, k)
+                x = as_dtype(x, torch.float16)
+                self._gemm_need = max(self._gemm_need, splits * rows * n)
+                self.launches.append(lambda x=x, w=weight, s=splits: kernels.qgemm_partial(x, w, splits=s,
+                                                                                           out=self.gemm_ws))
+                rt._count("rocm.qgemm_blocks")
+            else:
+                n, k = weight.shape
+                splits = 1
+                x = as_dtype(x, torch.float32)
+                self._gemm_need = max(self._gemm_need, rows * n)
+                self.launches.append(lambda x=x, w=weight: kernels.gemm_f32_partial(x, w, splits=1, out=self.gemm_ws))
+                rt._count("rocm.gemm_f32")
+            part = lambda s=splits, n=n: self.gemm_ws[: s * rows * n].view(s, rows, n)
+            return part, splits, n
+
+        for idx, node in enumerate(graph.nodes):
+            if idx in skip:
+                continue
+            op, ins, outs, attrs = node.op, node.inputs, node.outputs, node.attrs
+            if op == "token_embedding":
+                table = rt.weights.dense(ins[1], rt.dense_dtype)
+                out = buf(table.shape[1], torch.float32)
+                self.launches.append(lambda t=table, o=out: kernels.embedding(self.ids, t, torch.float32, out=o))
+                env[outs[0]] = out
+            elif op in _QKV_OPS:
+                layer = int(attrs.get("layer", 0))
+                x = env[ins[0]]
+                w_norm = rt.weights.dense(ins[1], rt.dense_dtype)
+                W = rt.weights.matmul_weight(tuple(ins[2:5]))
+                xn = buf(x.shape[1], gemm_dtype(W))
+                eps = float(attrs.get("eps", 1e-6))
+                self.launches.append(lambda x=x, w=w_norm, o=xn, e=eps: kernels.rmsnorm(x, w, e, o.dtype, out=o))
+                part, _, _ = gemm(xn, W)
+                cfg = rt.config
+                hd = int(attrs.get("head_dim", cfg.head_dim))
+                inv = rt.inv_freq(hd, float(attrs.get("rope_theta", cfg.rope_theta)))
+                q_out = buf(cfg.num_attention_heads * hd, rt.dtype)
+                kp, vp = rt.kv_allocator.layer_pools(layer)
+                self.launches.append(lambda part=part, inv=inv, q=q_out, kp=kp, vp=vp, hd=hd:
+                                     kernels.epilogue_qkv_rope_append(
+                                         part(), inv, self.positions, self.page_table, q, kp, vp, batch=self.batch,
+                                         q_len=self.q_len, num_heads=cfg.num_attention_heads,
+                                         num_kv_heads=cfg.num_key_value_heads, head_dim=hd))
+                rt._count("rocm.rmsnorm_qkv_rope_kv_append")
+                env[outs[0]], env[outs[1]], env[outs[2]] = q_out, ("kv-appended", layer), ("kv-appended", layer)
+            elif op in _ATTN_OPS:
+                layer = int(attrs.get("layer", 0))
+                if env.get(ins[1]) != ("kv-appended", layer) or env.get(ins[2]) != ("kv-appended", layer):
+                    raise NotImplementedError(
+                        f"{node.name}: attention whose K/V are not produced by fused_rmsnorm_qkv_rope of layer {layer}")
+                heads, hd = int(attrs["num_heads"]), int(attrs["head_dim"])
+                q = as_dtype(env[ins[0]], rt.dtype)
+                out = buf(heads * hd, rt.dtype)
+                kp, vp = rt.kv_allocator.layer_pools(layer)
+                decode = op == "paged_attention_decode" and self.q_len == 1
+                qv, ov = q.view(rows, heads, hd), out.view(rows, heads, hd)
+                if decode:
+                    self.launches.append(lambda qv=qv, ov=ov, kp=kp, vp=vp: kernels.paged_decode_attention(
+                        qv, kp, vp, self.page_table, self.seq_lens, out=ov, workspace=self.attn_ws))
+                else:
+                    self.launches.append(lambda qv=qv, ov=ov, kp=kp, vp=vp: kernels.paged_prefill_attention(
+                        qv, kp, vp, self.page_table, self.seq_lens, self.q_len, out=ov, workspace=self.attn_ws))
+                rt._count("rocm.paged_attention_decode" if decode else "rocm.paged_attention_prefill")
+                env[outs[0]] = out
+            elif op in _MATMUL_OPS:
+                W = rt.weights.matmul_weight((ins[1],))
+                part, _, n = gemm(env[ins[0]], W)
+                users = consumers.get(outs[0], [])
+                fuse = (len(users) == 1 and users[0].op == "add" and outs[0] in users[0].inputs
+                        and outs[0] not in graph.outputs)
+                if fuse:
+                    add = users[0]
+                    other = add.inputs[1] if add.inputs[0] == outs[0] else add.inputs[0]
+                    resid = as_dtype(env[other], torch.float32)
+                    out = buf(n, torch.float32)
+                    self.launches.append(lambda part=part, r=resid, o=out: kernels.epilogue_store(part(), o.dtype,
+                                                                                                  residual=r, out=o))
+                    env[add.outputs[0]] = out
+                    skip.add(graph.nodes.index(add))
+                else:
+                    out = buf(n, torch.float32)
+                    self.launches.append(lambda part=part, o=out: kernels.epilogue_store(part(), o.dtype, out=o))
+                    env[outs[0]] = out
+            elif op == "add":
+                a, b = as_dtype(env[ins[0]], torch.float32), as_dtype(env[ins[1]], torch.float32)
+                out = buf(a.shape[1], torch.float32)
+                self.launches.append(lambda a=a, b=b, o=out: kernels.add(a, b, out=o))
+                env[outs[0]] = out
+            elif op == "rms_norm":
+                x = env[ins[0]]
+                w = rt.weights.dense(ins[1], rt.dense_dtype)
+                odt = input_dtype_for(outs[0]) or torch.float32
+                out = buf(x.shape[1], odt)
+                eps = float(attrs.get("eps", 1e-6))
+                self.launches.append(lambda x=x, w=w, o=out, e=eps: kernels.rmsnorm(x, w, e, o.dtype, out=o))
+                env[outs[0]] = out
+            elif op in _SWIGLU_OPS:
+                W = rt.weights.matmul_weight((ins[1], ins[2]))
+                part, _, n2 = gemm(env[ins[0]], W)
+                odt = input_dtype_for(outs[0]) or torch.float32
+                out = buf(n2 // 2, odt)
+                self.launches.append(lambda part=part, o=out: kernels.epilogue_swiglu(part(), o.dtype, out=o))
+                rt._count("rocm.swiglu_epilogue")
+                env[outs[0]] = out
+            else:
+                raise NotImplementedError(f"HIP runtime does not implement op {op}")
+        logits = env[self.logits_name]
+        if not isinstance(logits, torch.Tensor):
+            raise NotImplementedError("graph output is not a tensor value")
+        self.logits = logits
+        self.next_ids = torch.zeros(rows, dtype=torch.int64, device=rt.device)
+
+    # ------------------------------------------------------------------ run ----
+    def set_inputs(self, ids: np.ndarray, page_rows: np.ndarray, positions: np.ndarray) -> None:
+        """Host -> device copies of the step inputs (into the static buffers)."""
+        self.ids.copy_(torch.from_numpy(np.ascontiguousarray(ids, dtype=np.int64).reshape(-1)))
+        self.page_table.copy_(torch.from_numpy(np.ascontiguousarray(page_rows, dtype=np.int32)))
+        pos = np.ascontiguousarray(positions, dtype=np.int32)
+        self.positions.copy_(torch.from_numpy(pos))
+        self.seq_lens.copy_(torch.from_numpy(pos + np.int32(self.q_len)))
+
+    def launch(self) -> None:
+        for fn in self.launches:
+            fn()
+
+    def launch_with_argmax(self) -> None:
+        self.launch()
+        kernels.argmax(self.logits, out=self.next_ids)
+
+    def capture(self, with_argmax: bool = True) -> torch.cuda.CUDAGraph:
+        """Capture the step into a HIP graph (after one eager warm-up on a side stream)."""
+        body = self.launch_with_argmax if with_argmax else self.launch
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            body()
+        torch.cuda.current_stream().wait_stream(side)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            body()
+        self.graph_obj = g
+        return g
+
+    def replay(self) -> None:
+        if self.graph_obj is None:
+            raise RuntimeError("plan has not been captured")
+        self.graph_obj.replay()
+
+
+# ========================================================================= runtime ==
+class HipRuntime:
+    """Execute compiled CacheIR graphs on an MI355X through the cacheir_amd HIP kernels."""
+
+    supports_variable_prefill_batch = True
+
+    def __init__(self, artifact: CompileArtifact | str | Path, *, device: str = "cuda", dtype: str | None = "auto",
+                 weights: HipWeightStore | None = None, source=None, tokenizer=None,
+                 prefix_cache: PrefixCache | None = None, kv_allocator: HipKVPageAllocator | None = None,
+                 kv_capacity_pages: int = 64, memory_limit_mb: float | None = None,
+                 _plans: dict | None = None, _inv_freq: dict | None = None):
+        if not torch.cuda.is_available():
+            raise RuntimeError("HipRuntime requested a GPU, but torch.cuda.is_available() is false")
+        hip.load()  # no CPU fallback: fail here if the kernel library is missing
+        self.artifact = CompileArtifact.load(artifact) if isinstance(artifact, (str, Path)) else artifact
+        self.config = self.artifact.config
+        self.device = torch.device(device)
+        graph = self.artifact.graph("decode")
+        quant = (self.artifact.quant or "").lower() or None
+        if weights is None:
+            source = source if source is not None else self._open_source()
+            blocked = quant in {"q4_0", "q8_0"} or isinstance(source, (GGUFSource, SyntheticQuant))
+            self.dtype = self._select_dtype(dtype, blocked)
+            dense_dtype = torch.float16 if self.dtype == torch.float16 else torch.float32
+            weights = HipWeightStore(source, graph.weights, device=self.device, dense_dtype=dense_dtype, quant=quant)
+        else:
+            self.dtype = self._select_dtype(dtype, weights.dense_dtype == torch.float16)
+        self.weights = weights
+        self.dense_dtype = weights.dense_dtype
+        self.tokenizer = tokenizer or ByteTokenizer(self.config.vocab_size)
+        page_size = int(graph.attrs.get("execution_hints", {}).get("page_size", 16))
+        self.kv_allocator = kv_allocator or HipKVPageAllocator(
+            num_layers=self.config.num_layers, kv_heads=self.config.num_key_value_heads, head_dim=self.config.head_dim,
+            page_size=page_size, dtype=self.dtype, device=self.device, capacity_pages=kv_capacity_pages)
+        if self.kv_allocator.dtype != self.dtype:
+            raise ValueError("kv_allocator dtype differs from the runtime dtype")
+        self.kv_cache = HipPagedKVCache(self.kv_allocator)
+        self.prefix_cache = prefix_cache or PrefixCache(capacity=8)
+        self.memory_limit_mb = memory_limit_mb
+        self._plans: dict = _plans if _plans is not None else {}
+        self._inv_freq: dict = _inv_freq if _inv_freq is not None else {}
+        self.kernel_counts: OrderedDict[str, int] = OrderedDict()
+        self.oom_recoveries = 0
+
+    # ------------------------------------------------------------- helpers --
+    def _open_source(self):
+        path = Path(self.artifact.model_path)
+        if path.suffix == ".gguf":
+            return GGUFSource(path, gguf_key_map(self.config.num_layers))
+        if path.is_dir() or path.suffix == ".npz":
+            return NpzDir(path)
+        raise FileNotFoundError(f"no weights found for model_path {str(path)!r}; pass source= or weights=")
+
+    def _select_dtype(self, name: str | None, blocked: bool) -> torch.dtype:
+        if name in (None, "auto"):
+            half = blocked or str(self.config.dtype).lower() in {"float16", "fp16", "bfloat16", "bf16"}
+            return torch.float16 if half else torch.float32
+        table = {"float16": torch.float16, "fp16": torch.float16, "float32": torch.float32, "fp32": torch.float32}
+        if name.lower() not in table:
+            raise ValueError(f"Unsupported HIP runtime dtype {name!r} (float16 or float32)")
+        return table[name.lower()]
+
+    def _count(self, name: str) -> None:
+        self.kernel_counts[name] = self.kernel_counts.get(name, 0) + 1
+
+    def inv_freq(self, head_dim: int, theta: float) -> torch.Tensor:
+        key = (head_dim, float(theta))
+        if key not in self._inv_freq:
+            self._inv_freq[key] = torch.from_numpy(rope_inv_freq(head_dim, theta)).to(self.device)
+        return self._inv_freq[key]
+
+    def plan(self, mode: str, batch: int, q_len: int, max_pages: int) -> StepPlan:
+        key = (mode, batch, q_len, max_pages)
+        plan = self._plans.get(key)
+        if plan is None or plan.generation != self.kv_allocator.generation:
+            plan = StepPlan(self, mode, batch, q_len, max_pages)
+            self._plans[key] = plan
+        return plan
+
+    @staticmethod
+    def _bucket(pages: int) -> int:
+        b = 4
+        while b < pages:
+            b *= 2
+        return b
+
+    def _enforce_memory_limit(self) -> None:
+        if self.memory_limit_mb is None:
+            return
+        mb = torch.cuda.memory_allocated(self.device) / (1024.0 * 1024.0)
+        if mb > float(self.memory_limit_mb):
+            self._recover_from_oom()
+            raise RuntimeError(f"CacheIR HIP memory limit exceeded: {mb:.1f} MB allocated, limit "
+                               f"{float(self.memory_limit_mb):.1f} MB")
+
+    def _recover_from_oom(self) -> None:
+        self.oom_recoveries += 1
+        self.kv_cache.clear()
+        self._plans.clear()
+        torch.cuda.empty_cache()
+
+    # -------------------------------------------------------------- API -----
+    @classmethod
+    def available(cls) -> bool:
+        return hip_runtime_available()
+
+    def fork(self) -> "HipRuntime":
+        """New session sharing artifact, weights, tokenizer, prefix cache, plans and the KV allocator."""
+        return HipRuntime(self.artifact, device=str(self.device), dtype=self._dtype_name(), weights=self.weights,
+                          tokenizer=self.tokenizer, prefix_cache=self.prefix_cache, kv_allocator=self.kv_allocator,
+                          memory_limit_mb=self.memory_limit_mb, _plans=self._plans, _inv_freq=self._inv_freq)
+
+    def _dtype_name(self) -> str:
+        return "float16" if self.dtype == torch.float16 else "float32"
+
+    def _execute(self, sessions: list["HipRuntime"], ids: np.ndarray, mode: str) -> torch.Tensor:
+        batch, q_len = ids.shape
+        P = self.kv_allocator.page_size
+        need_pages = sum(max(0, -(-(s.kv_cache.tokens + q_len) // P) - len(s.kv_cache.slots)) for s in sessions)
+        self.kv_allocator.reserve(need_pages)  # grow (and re-base pools) before any plan is built
+        positions = np.array([s.kv_cache.tokens for s in sessions], dtype=np.int32)
+        for s in sessions:
+            s.kv_cache.ensure_capacity(s.kv_cache.tokens + q_len)
+        max_pages = self._bucket(max(len(s.kv_cache.slots) for s in sessions))
+        rows = np.zeros((batch, max_pages), dtype=np.int32)
+        for b, s in enumerate(sessions):
+            rows[b, : len(s.kv_cache.slots)] = s.kv_cache.slots
+        self._enforce_memory_limit()
+        try:
+            plan = self.plan(mode, batch, q_len, max_pages)
+            plan.set_inputs(ids, rows, positions)
+            plan.launch()
+        except torch.cuda.OutOfMemoryError as exc:
+            self._recover_from_oom()
+            raise RuntimeError("CacheIR HIP runtime recovered from an out-of-memory condition; "
+                               "retry with a smaller batch/context") from exc
+        for s in sessions:
+            s.kv_cache.tokens += q_len
+        return plan.logits.view(batch, q_len, -1).clone()
+
+    def run(self, input_ids, *, mode: str = "prefill", reset_kv: bool | None = None) -> torch.Tensor:
+        if reset_kv is None:
+            reset_kv = mode == "prefill"
+        if mode == "prefill" and reset_kv:
+            self.kv_cache.clear()
+        ids = np.asarray(input_ids, dtype=np.int64)
+        if ids.ndim == 1:
+            ids = ids[None, :]
+        if ids.ndim != 2 or ids.shape[0] != 1 or ids.shape[1] < 1:
+            raise ValueError("HipRuntime.run takes one sequence [1, seq]; use run_decode_batch / run_prefill_batch "
+                             "for several sessions")
+        if mode == "decode" and ids.shape[1] != 1:
+            raise ValueError("decode mode takes exactly one token per step")
+        return self._execute([self], ids, mode)
+
+    def _check_sessions(self, sessions) -> None:
+        if not sessions:
+            raise ValueError("batch requires at least one session")
+        for s in sessions:
+            if not isinstance(s, HipRuntime):
+                raise TypeError("only HipRuntime sessions can be batched")
+            if s.artifact is not self.artifact and s.artifact.to_dict() != self.artifact.to_dict():
+                raise ValueError("all HIP sessions must use the same CacheIR artifact")
+            if s.device != self.device:
+                raise ValueError("all HIP sessions must use the same device")
+            if s.kv_allocator is not self.kv_allocator:
+                raise ValueError("all HIP sessions must share one KV allocator (create them with fork())")
+
+    def run_decode_batch(self, sessions: list["HipRuntime"], token_ids) -> torch.Tensor:
+        """One decode token for several sessions in one launch sequence -> logits ``[B, 1, V]``."""
+        if not sessions:
+            raise ValueError("run_decode_batch requires at least one session")
+        if len(sessions) != len(token_ids):
+            raise ValueError("sessions and token_ids must have the same length")
+        self._check_sessions(sessions)
+        ids = np.array([[int(t)] for t in token_ids], dtype=np.int64)
+        self._count("cacheir.rocm_decode_batch_graph")
+        return self._execute(list(sessions), ids, "decode")
+
+    def run_prefill_batch(self, sessions: list["HipRuntime"], token_id_batches: list[list[int]]) -> torch.Tensor:
+        """Prefill several sessions -> logits ``[B, max_len, V]`` (rows past a prompt's end are zero)."""
+        if not sessions:
+            raise ValueError("run_prefill_batch requires at least one session")
+        if len(sessions) != len(token_id_batches):
+            raise ValueError("sessions and token_id_batches must have the same length")
+        lens = [len(t) for t in token_id_batches]
+        if any(n <= 0 for n in lens):
+            raise ValueError("run_prefill_batch requires non-empty token batches")
+        self._check_sessions(sessions)
+        for s in sessions:
+            s.kv_cache.clear()
+        self._count("cacheir.rocm_prefill_batch_graph")
+        if len(set(lens)) == 1:
+            return self._execute(list(sessions), np.array(token_id_batches, dtype=np.int64), "prefill")
+        out = torch.zeros((len(sessions), max(lens), self.config.vocab_size), dtype=torch.float32, device=self.device)
+        for b, (s, toks) in enumerate(zip(sessions, token_id_batches)):
+            out[b, : len(toks)] = s._execute([s], np.array([toks], dtype=np.int64), "prefill")[0]
+        return out
+
+    def prefill_tokens(self, token_ids, *, use_prefix_cache: bool = False, remember_prefix: bool = False):
+        ids = [int(t) for t in token_ids]
+        logits = self.run([ids], mode="prefill", reset_kv=True)
+        return logits, ()
+
+    def generate_ids(self, prompt_ids, max_new_tokens: int = 16) -> list[int]:
+        logits = self.run([list(prompt_ids)], mode="prefill", reset_kv=True)
+        out = []
+        for _ in range(max_new_tokens):
+            nxt = int(torch.argmax(logits[0, -1]).item()) % self.config.vocab_size
+            out.append(nxt)
+            logits = self.run([[nxt]], mode="decode")
+        return out
+
+    def generate(self, prompt: str, *, max_new_tokens: int = 16, use_prefix_cache: bool = False,
+                 remember_prefix: bool = True):
+        ids = self.tokenizer.encode(prompt)
+        logits, _ = self.prefill_tokens(ids)
+        for _ in range(max_new_tokens):
+            nxt = int(torch.argmax(logits[0, -1]).item()) % self.config.vocab_size
+            yield self.tokenizer.decode([nxt])
+            logits = self.run([[nxt]], mode="decode")
+
+    def synchronize(self) -> None:
+        torch.cuda.synchronize(self.device)
+
+    def cache_stats(self) -> dict[str, object]:
+        stats = self.kv_cache.stats()
+        stats["prefix_cache"] = self.prefix_cache.stats()
+        stats["kernel_counts"] = dict(self.kernel_counts)
+        stats["oom_recoveries"] = self.oom_recoveries
+        stats["memory_limit_mb"] = self.memory_limit_mb
+        stats["weight_bytes"] = self.weights.nbytes()
+        return stats

@@ -245,7 +245,7 @@ class HipWeightStore:
             if isinstance(self.source, SyntheticQuant):
                 t = self.source.dense_device(spec.key, dtype)
             else:
-                arr = np.ascontiguousarray(self.source.dense(spec.key))
+                arr = np.array(self.source.dense(spec.key), copy=True, order="C")
                 t = torch.from_numpy(arr).to(self.device).to(dtype)
             self._dense[key] = t.contiguous()
         return self._dense[key]

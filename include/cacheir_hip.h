@@ -134,6 +134,9 @@ int cir_rmsnorm(const void* x, int xdt, const void* w, int wdt, void* out, int o
 /* out = a + b elementwise (graph op "add"), all of dtype dt. */
 int cir_add(const void* a, const void* b, void* out, int dt, size_t count, void* stream);
 
+/* out = in converted between dtypes (idt -> odt); count elements. */
+int cir_cast(const void* in, int idt, void* out, int odt, size_t count, void* stream);
+
 /* Greedy sampling (cpu.py:181-182, scheduler.py:535-543): ids[r] = first index of
  * the maximum of logits[r][0:vocab] (fp32, row stride ld). */
 int cir_argmax(const float* logits, int ld, int64_t* ids, int rows, int vocab, void* stream);

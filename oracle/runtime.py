@@ -153,3 +153,49 @@ def generate_ids(rt: OracleRuntime, prompt_ids: list[int], max_new_tokens: int) 
 def decode_batch(sessions: list[OracleRuntime], token_ids: list[int]) -> np.ndarray:
     """Sequential per-session decode, stacked ``[B, 1, V]``."""
     return np.concatenate([s.run([[int(t)]], mode="decode") for s, t in zip(sessions, token_ids)], axis=0)
+
+
+def direct_generate(w: dict[str, np.ndarray], *, num_layers: int, num_heads: int, num_kv_heads: int, eps: float,
+                    theta: float, vocab: int, prompt_ids: list[int], max_new_tokens: int) -> tuple[list[int], list[np.ndarray]]:
+    """Llama decoder written out directly (no graph): the per-layer sequence of
+    ``cacheir/importers/hf.py:196-266`` with the op semantics of ``cpu.py:221-377``.
+
+    Used to pin the graph builder's wiring: graph-driven and direct generation must
+    agree.  Returns the greedy ids and the logits row of every step.
+    """
+    hidden = w["model.embed_tokens.weight"].shape[1]
+    hd = hidden // num_heads
+    cache_k: dict[int, np.ndarray] = {}
+    cache_v: dict[int, np.ndarray] = {}
+
+    def forward(ids: np.ndarray, causal: bool) -> np.ndarray:
+        x = w["model.embed_tokens.weight"][ids]
+        for layer in range(num_layers):
+            p = f"model.layers.{layer}"
+            h = ops.rms_norm(x, w[f"{p}.input_layernorm.weight"], eps)
+            q = ops.matmul(h, w[f"{p}.self_attn.q_proj.weight"])
+            k = ops.matmul(h, w[f"{p}.self_attn.k_proj.weight"])
+            v = ops.matmul(h, w[f"{p}.self_attn.v_proj.weight"])
+            off = cache_k[layer].shape[1] if layer in cache_k else 0
+            q, k = ops.rope_one(q, hd, theta, off), ops.rope_one(k, hd, theta, off)
+            b, s, _ = q.shape
+            kh, vh = k.reshape(b, s, num_kv_heads, hd), v.reshape(b, s, num_kv_heads, hd)
+            cache_k[layer] = kh if layer not in cache_k else np.concatenate([cache_k[layer], kh], axis=1)
+            cache_v[layer] = vh if layer not in cache_v else np.concatenate([cache_v[layer], vh], axis=1)
+            a = ops.attention(q.reshape(b, s, num_heads, hd), cache_k[layer], cache_v[layer], num_heads, num_kv_heads,
+                              hd, causal=causal)
+            x = x + ops.matmul(a, w[f"{p}.self_attn.o_proj.weight"])
+            h = ops.rms_norm(x, w[f"{p}.post_attention_layernorm.weight"], eps)
+            g = ops.silu_mul(ops.matmul(h, w[f"{p}.mlp.gate_proj.weight"]), ops.matmul(h, w[f"{p}.mlp.up_proj.weight"]))
+            x = x + ops.matmul(g, w[f"{p}.mlp.down_proj.weight"])
+        x = ops.rms_norm(x, w["model.norm.weight"], eps)
+        return ops.matmul(x, w["lm_head.weight"])
+
+    logits = forward(np.asarray([prompt_ids], dtype=np.int64), causal=True)
+    rows, out = [], []
+    for _ in range(max_new_tokens):
+        rows.append(logits[0, -1].copy())
+        nxt = int(np.argmax(logits[0, -1])) % vocab
+        out.append(nxt)
+        logits = forward(np.asarray([[nxt]], dtype=np.int64), causal=False)
+    return out, rows

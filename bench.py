@@ -1,0 +1,195 @@
+"""Decode-step benchmark for the MI355X backend (BASELINE.json metric).
+
+Workload (one GPU): Llama-3-8B-shaped decoder -- 32 layers, hidden
+4096, 32 query / 8 KV heads (head_dim 128), SwiGLU ffn 14336, vocab 128256, every
+linear weight (QKV, O, gate, up, down, lm_head) Q4_0 blocks, norms and embeddings
+fp16, random-init weights generated on the device.  Batch 32, every sequence at 2048
+tokens of context (2047 cached + the new one), page size 16, greedy sampling.  The KV
+pages hold synthetic N(0,1) fp16 values (no prompt is prefilled; the measured step
+is a real decode step over that paged context).
+
+A "step" = one HIP-graph replay of the whole decode graph: token embedding, 32 x
+(RMSNorm + QKV GEMM + RoPE/KV-append, paged attention, O GEMM + residual, RMSNorm +
+gate|up GEMM + SwiGLU, down GEMM + residual), final norm, lm_head GEMM, argmax, and the
+copy of the argmax ids into the next step's input.  Positions are held at 2047, so
+every step re-appends at the same slot and attends over exactly 2048 tokens.
+
+Printed: one JSON line with value = decode tokens/s (32 tokens per step), the
+paged-attention roofline (algorithmic bytes / live HIP-event time of the attention
+kernel, rotated over the 32 layers' KV so the 256 MB MALL cannot hold it), and a
+CPU baseline (the C/OpenMP oracle restatement timed on this host over one layer
+and the lm_head, scaled to a full step).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+HBM_PEAK_GBS = 8000.0
+
+
+def parse() -> argparse.Namespace:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--batch", type=int, default=32)
+    ap.add_argument("--ctx", type=int, default=2048)
+    ap.add_argument("--layers", type=int, default=32)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--attn-iters", type=int, default=64)
+    return ap.parse_args()
+
+
+def llama3_8b(layers: int):
+    from cacheir_amd.artifact import ModelConfig
+
+    return ModelConfig(architecture="Llama3-8B-shape", hidden_size=4096, intermediate_size=14336, num_layers=layers,
+                       num_attention_heads=32, num_key_value_heads=8, vocab_size=128256,
+                       max_position_embeddings=8192, rope_theta=500000.0, rms_norm_eps=1e-5, dtype="float16")
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def main() -> int:
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); this build has no multi-GPU path",
+              flush=True)
+        return 2
+    import torch
+
+    from cacheir_amd.compiler import compile_config
+    from cacheir_amd.runtime import HipRuntime
+    from cacheir_amd.weights import GGML_Q4_0, SyntheticQuant
+
+    dev = torch.device("cuda:0")
+    cfg = llama3_8b(args.layers)
+    B, ctx, P = args.batch, args.ctx, 16
+    art = compile_config(cfg, quant="q4_0", modes=("decode",))
+    pages_per_seq = -(-ctx // P)
+    t0 = time.time()
+    base = HipRuntime(art, source=SyntheticQuant(GGML_Q4_0, dev, seed=0),
+                      kv_capacity_pages=B * pages_per_seq + 8)
+    sessions = [base.fork() for _ in range(B)]
+    for s in sessions:
+        s.kv_cache.ensure_capacity(ctx)
+        s.kv_cache.tokens = ctx - 1
+    g = torch.Generator(device=dev)
+    g.manual_seed(1)
+    for layer in range(cfg.num_layers):  # synthetic context: N(0,1) fp16 K/V in every page
+        base.kv_allocator.k[layer].normal_(generator=g)
+        base.kv_allocator.v[layer].normal_(generator=g)
+    max_pages = base._bucket(pages_per_seq)
+    plan = base.plan("decode", B, 1, max_pages)
+    rows = np.zeros((B, max_pages), np.int32)
+    for b, s in enumerate(sessions):
+        rows[b, : len(s.kv_cache.slots)] = s.kv_cache.slots
+    ids = np.random.default_rng(0).integers(0, cfg.vocab_size, size=(B, 1))
+    plan.set_inputs(ids, rows, np.full(B, ctx - 1, np.int32))
+    torch.cuda.synchronize()
+    log(f"model ready in {time.time() - t0:.1f}s; weights {base.weights.nbytes() / 1e9:.3f} GB, "
+        f"KV pool {base.kv_allocator.stats()['persistent_pools'][0]['bytes'] / 1e9:.3f} GB")
+
+    def body():
+        plan.launch_with_argmax()
+        plan.ids.copy_(plan.next_ids)
+
+    # capture (warm-up on a side stream first, as torch requires)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        body()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        body()
+    for _ in range(args.warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    log("warm-up done")
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(args.steps):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    ms_step = start.elapsed_time(end) / args.steps
+    toks = B * 1000.0 / ms_step
+    assert torch.isfinite(plan.logits).all().item(), "non-finite logits"
+    log(f"step {ms_step:.3f} ms -> {toks:.1f} tok/s")
+
+    # ---- live roofline of the paged-attention kernel (HIP events on the launch stream) ----
+    from cacheir_amd import kernels
+
+    H, Hkv, D = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+    q = torch.randn((B, H, D), device=dev, dtype=torch.float16)
+    out = torch.empty_like(q)
+    ws = kernels.attention_workspace(B, H, D, max_pages * P, dev)
+    stream = torch.cuda.current_stream()
+    for layer in range(min(4, cfg.num_layers)):
+        kp, vp = base.kv_allocator.layer_pools(layer)
+        kernels.paged_decode_attention(q, kp, vp, plan.page_table, plan.seq_lens, out=out, workspace=ws)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for it in range(args.attn_iters):
+        kp, vp = base.kv_allocator.layer_pools(it % cfg.num_layers)
+        kernels.paged_decode_attention(q, kp, vp, plan.page_table, plan.seq_lens, out=out, workspace=ws)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    attn_us = e0.elapsed_time(e1) * 1000.0 / args.attn_iters
+    kv_bytes = 2 * Hkv * D * 2 * B * ctx  # K + V fp16 over every visible token
+    qo_bytes = 2 * B * H * D * 2
+    table_bytes = 4 * B * pages_per_seq + 4 * B
+    attn_bytes = kv_bytes + qo_bytes + table_bytes
+    achieved = attn_bytes / (attn_us * 1e-6) / 1e9
+    log(f"attention {attn_us:.2f} us/launch, {achieved:.0f} GB/s ({achieved / HBM_PEAK_GBS:.1%} of peak)")
+
+    # ---- CPU baseline: C/OpenMP restatement, one layer + lm_head, scaled to the step ----
+    cpu = None
+    if not args.no_cpu:
+        from oracle import cbase
+
+        cpu = cbase.time_decode_step(batch=B, ctx=ctx, hidden=4096, ffn=14336, heads=H, kv_heads=Hkv, vocab=128256,
+                                     layers=cfg.num_layers, budget_s=12.0, log=log)
+
+    weight_bytes = base.weights.nbytes()
+    line = {
+        "metric": "decode tokens/s, batch 32, Llama-3-8B-shape Q4_0; paged-attn HBM GB/s",
+        "value": round(toks, 2),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16 activations/KV, Q4_0 weights (int4 x fp16 MFMA, fp32 accumulate)",
+        "data": "synthetic: random-init Q4_0 weights, N(0,1) fp16 KV context",
+        "config": {"workload": "BASELINE config 4: Llama-3-8B-shape Q4_0 full decode step", "batch": B,
+                   "context": ctx, "layers": cfg.num_layers, "page_size": P, "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "kernel": "paged decode attention (attn_chunk_f16_d128<4>)",
+                     "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "bytes_per_launch": attn_bytes, "us_per_launch": round(attn_us, 3)},
+        "step_bytes": {"weights": weight_bytes, "kv": kv_bytes * cfg.num_layers,
+                       "hbm_floor_ms": round((weight_bytes + kv_bytes * cfg.num_layers) / HBM_PEAK_GBS / 1e6, 4)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

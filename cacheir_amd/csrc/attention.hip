@@ -41,19 +41,67 @@ __device__ __forceinline__ int visible_len(const int32_t* lens, int row, int q_l
   return min(lens[b] - q_len + s + 1, max_ctx);
 }
 
+// Merge the chunks of heads [head0, head0 + nh) of one row:
+// out = sum_c 2^(m_c - M) O_c / sum_c 2^(m_c - M) l_c.  One wavefront.
+template <typename T>
+__device__ void merge_chunks(const float* __restrict__ part_o, const float* __restrict__ part_ml, T* __restrict__ out,
+                             int row, int head0, int nh, int Hq, int D, int NC, int nc, int lane) {
+  for (int h = 0; h < nh; ++h) {
+    const int head = head0 + h;
+    const float* ml = part_ml + ((size_t)row * Hq + head) * NC * 2;
+    float M = -INFINITY;
+    for (int c = 0; c < nc; ++c) M = fmaxf(M, ml[2 * c]);
+    float denom = 0.f;
+    for (int c = 0; c < nc; ++c) denom += ml[2 * c + 1] * exp2f(ml[2 * c] - M);
+    const float inv = denom > 0.f ? 1.f / denom : 0.f;
+    const float* po = part_o + ((size_t)row * Hq + head) * NC * D;
+    for (int d = lane; d < D; d += 64) {
+      float o = 0.f;
+      for (int c = 0; c < nc; ++c) o = fmaf(po[(size_t)c * D + d], exp2f(ml[2 * c] - M), o);
+      out[((size_t)row * Hq + head) * D + d] = from_f32<T>(o * inv);
+    }
+  }
+}
+
+// Called by every wavefront after it stored its chunk.  The wavefront that takes the
+// last ticket of (row, kvh) merges all chunks and resets the counter to zero.
+template <typename T>
+__device__ void finish_chunk(const float* part_o, const float* part_ml, int* counters, T* out, int row, int kvh,
+                             int G, int Hq, int Hkv, int D, int NC, int L, int lane) {
+  __threadfence();  // publish this chunk's partials (agent-scope release)
+  int ticket = 0;
+  if (lane == 0) ticket = atomicAdd(&counters[(size_t)row * Hkv + kvh], 1);
+  ticket = __shfl(ticket, 0, 64);
+  const int nc = (L + kChunk - 1) / kChunk;
+  if (ticket != nc - 1) return;
+  __threadfence();  // acquire: see every other chunk's partials
+  merge_chunks<T>(part_o, part_ml, out, row, kvh * G, G, Hq, D, NC, nc, lane);
+  if (lane == 0) counters[(size_t)row * Hkv + kvh] = 0;
+}
+
+// A row with nothing visible (seq_len 0) gets zeros from its chunk-0 wavefront.
+template <typename T>
+__device__ void zero_heads(T* out, int row, int head0, int nh, int Hq, int D, int lane) {
+  for (int h = 0; h < nh; ++h)
+    for (int d = lane; d < D; d += 64) out[((size_t)row * Hq + head0 + h) * D + d] = from_f32<T>(0.f);
+}
+
 // ----------------------------------------------------------------------------
 // fp16 pools, head_dim 128, MFMA scores.  G = query heads per KV head (1..8).
 template <int G>
 __global__ __launch_bounds__(64) void attn_chunk_f16_d128(
     const f16* __restrict__ q, const f16* __restrict__ kp, const f16* __restrict__ vp,
     const int32_t* __restrict__ pt, const int32_t* __restrict__ lens,
-    float* __restrict__ part_o, float* __restrict__ part_ml,
+    float* __restrict__ part_o, float* __restrict__ part_ml, int* __restrict__ counters, f16* __restrict__ out,
     int q_len, int Hq, int Hkv, int P, int max_pages, int NC, float scale_log2) {
   constexpr int D = 128;
   const int chunk = blockIdx.x, kvh = blockIdx.y, row = blockIdx.z;
   const int L = visible_len(lens, row, q_len, max_pages * P);
   const int t0 = chunk * kChunk;
-  if (t0 >= L) return;
+  if (t0 >= L) {
+    if (chunk == 0) zero_heads<f16>(out, row, kvh * G, G, Hq, D, threadIdx.x);
+    return;
+  }
   const int t1 = min(L, t0 + kChunk);
   const int b = row / q_len;
   const int lane = threadIdx.x;
@@ -184,6 +232,7 @@ __global__ __launch_bounds__(64) void attn_chunk_f16_d128(
       }
     }
   }
+  finish_chunk<f16>(part_o, part_ml, counters, out, row, kvh, G, Hq, Hkv, D, NC, L, lane);
 }
 
 // ----------------------------------------------------------------------------
@@ -192,18 +241,21 @@ template <typename T>
 __global__ __launch_bounds__(64) void attn_chunk_generic(
     const T* __restrict__ q, const T* __restrict__ kp, const T* __restrict__ vp,
     const int32_t* __restrict__ pt, const int32_t* __restrict__ lens,
-    float* __restrict__ part_o, float* __restrict__ part_ml,
+    float* __restrict__ part_o, float* __restrict__ part_ml, int* __restrict__ counters, T* __restrict__ out,
     int q_len, int Hq, int Hkv, int D, int P, int max_pages, int NC, float scale_log2) {
   __shared__ float qs[256];
   __shared__ float ps[kChunk];
   const int chunk = blockIdx.x, kvh = blockIdx.y, row = blockIdx.z;
   const int L = visible_len(lens, row, q_len, max_pages * P);
   const int t0 = chunk * kChunk;
-  if (t0 >= L) return;
-  const int n = min(L, t0 + kChunk) - t0;
-  const int b = row / q_len;
   const int G = Hq / Hkv;
   const int lane = threadIdx.x;
+  if (t0 >= L) {
+    if (chunk == 0) zero_heads<T>(out, row, kvh * G, G, Hq, D, lane);
+    return;
+  }
+  const int n = min(L, t0 + kChunk) - t0;
+  const int b = row / q_len;
   const int32_t* ptrow = pt + (size_t)b * max_pages;
   for (int h = 0; h < G; ++h) {
     const int head = kvh * G + h;
@@ -245,29 +297,7 @@ __global__ __launch_bounds__(64) void attn_chunk_generic(
       ml[1] = sum;
     }
   }
-}
-
-// ----------------------------------------------------------------------------
-// Merge the chunks of one (row, head): out = sum_c 2^(m_c - M) O_c / sum_c 2^(m_c - M) l_c.
-template <typename T>
-__global__ __launch_bounds__(128) void attn_combine(
-    const float* __restrict__ part_o, const float* __restrict__ part_ml, const int32_t* __restrict__ lens,
-    T* __restrict__ out, int q_len, int Hq, int D, int NC, int max_ctx) {
-  const int head = blockIdx.x, row = blockIdx.y;
-  const int L = visible_len(lens, row, q_len, max_ctx);
-  const int nc = L > 0 ? min(NC, (L + kChunk - 1) / kChunk) : 0;
-  const float* ml = part_ml + ((size_t)row * Hq + head) * NC * 2;
-  float M = -INFINITY;
-  for (int c = 0; c < nc; ++c) M = fmaxf(M, ml[2 * c]);
-  float denom = 0.f;
-  for (int c = 0; c < nc; ++c) denom += ml[2 * c + 1] * exp2f(ml[2 * c] - M);
-  const float inv = denom > 0.f ? 1.f / denom : 0.f;
-  const float* po = part_o + ((size_t)row * Hq + head) * NC * D;
-  for (int d = threadIdx.x; d < D; d += blockDim.x) {
-    float o = 0.f;
-    for (int c = 0; c < nc; ++c) o = fmaf(po[(size_t)c * D + d], exp2f(ml[2 * c] - M), o);
-    out[((size_t)row * Hq + head) * D + d] = from_f32<T>(o * inv);
-  }
+  finish_chunk<T>(part_o, part_ml, counters, out, row, kvh, G, Hq, Hkv, D, NC, L, lane);
 }
 
 int num_chunks(int max_context) { return max_context > 0 ? (max_context + kChunk - 1) / kChunk : 1; }
@@ -290,6 +320,7 @@ int launch_attention(const void* q, const void* k_pool, const void* v_pool, cons
   CIR_CHECK_ARG(rows <= 65535 && Hkv <= 65535, "attention: grid too large");
   float* part_o = static_cast<float*>(workspace);
   float* part_ml = part_o + (size_t)rows * Hq * NC * D;
+  int* counters = reinterpret_cast<int*>(part_ml + (size_t)rows * Hq * NC * 2);
   const float scale_log2 = scale * kLog2e;
   const int G = Hq / Hkv;
   hipStream_t s = as_stream(stream);
@@ -301,8 +332,9 @@ int launch_attention(const void* q, const void* k_pool, const void* v_pool, cons
     auto kv = static_cast<const f16*>(v_pool);
 #define CIR_ATT_CASE(g)                                                                                    \
   case g:                                                                                                  \
-    attn_chunk_f16_d128<g><<<grid, 64, 0, s>>>(kq, kk, kv, page_table, seq_lens, part_o, part_ml, q_len, Hq, \
-                                               Hkv, P, max_pages, NC, scale_log2);                         \
+    attn_chunk_f16_d128<g><<<grid, 64, 0, s>>>(kq, kk, kv, page_table, seq_lens, part_o, part_ml, counters,   \
+                                               static_cast<f16*>(out), q_len, Hq, Hkv, P, max_pages, NC,  \
+                                               scale_log2);                                                \
     break;
     switch (G) {
       CIR_ATT_CASE(1) CIR_ATT_CASE(2) CIR_ATT_CASE(3) CIR_ATT_CASE(4)
@@ -312,19 +344,13 @@ int launch_attention(const void* q, const void* k_pool, const void* v_pool, cons
   } else if (kv_dtype == CIR_F16) {
     attn_chunk_generic<f16><<<grid, 64, 0, s>>>(static_cast<const f16*>(q), static_cast<const f16*>(k_pool),
                                                 static_cast<const f16*>(v_pool), page_table, seq_lens, part_o,
-                                                part_ml, q_len, Hq, Hkv, D, P, max_pages, NC, scale_log2);
+                                                part_ml, counters, static_cast<f16*>(out), q_len, Hq, Hkv, D, P,
+                                                max_pages, NC, scale_log2);
   } else {
     attn_chunk_generic<float><<<grid, 64, 0, s>>>(static_cast<const float*>(q), static_cast<const float*>(k_pool),
                                                   static_cast<const float*>(v_pool), page_table, seq_lens, part_o,
-                                                  part_ml, q_len, Hq, Hkv, D, P, max_pages, NC, scale_log2);
-  }
-  int st = launch_status();
-  if (st) return st;
-  dim3 cgrid(Hq, rows);
-  if (kv_dtype == CIR_F16) {
-    attn_combine<f16><<<cgrid, 128, 0, s>>>(part_o, part_ml, seq_lens, static_cast<f16*>(out), q_len, Hq, D, NC, max_pages * P);
-  } else {
-    attn_combine<float><<<cgrid, 128, 0, s>>>(part_o, part_ml, seq_lens, static_cast<float*>(out), q_len, Hq, D, NC, max_pages * P);
+                                                  part_ml, counters, static_cast<float*>(out), q_len, Hq, Hkv, D, P,
+                                                  max_pages, NC, scale_log2);
   }
   return launch_status();
 }
@@ -335,7 +361,8 @@ int launch_attention(const void* q, const void* k_pool, const void* v_pool, cons
 extern "C" size_t cir_paged_attention_workspace_bytes(int rows, int num_heads, int head_dim, int max_context) {
   if (rows <= 0 || num_heads <= 0 || head_dim <= 0) return 0;
   const size_t nc = (size_t)cir::num_chunks(max_context);
-  return (size_t)rows * num_heads * nc * ((size_t)head_dim + 2) * sizeof(float);
+  // partial O and (max, sum) per (row, head, chunk), then one ticket counter per (row, head)
+  return (size_t)rows * num_heads * nc * ((size_t)head_dim + 2) * sizeof(float) + (size_t)rows * num_heads * sizeof(int);
 }
 
 extern "C" int cir_paged_decode_attention(const void* q, const void* k_pool, const void* v_pool,

@@ -35,7 +35,7 @@ def _cuda(t: torch.Tensor, name: str) -> None:
 # ------------------------------------------------------------------ attention --
 def attention_workspace(rows: int, num_heads: int, head_dim: int, max_context: int, device) -> torch.Tensor:
     n = hip.size_call("cir_paged_attention_workspace_bytes", rows, num_heads, head_dim, max_context)
-    return torch.empty(max(n, 4), dtype=torch.uint8, device=device)
+    return torch.zeros(max(n, 4), dtype=torch.uint8, device=device)  # ticket counters must start at zero
 
 
 def _check_pool(q, k_pool, v_pool, page_table, seq_lens, num_heads, check_tables):

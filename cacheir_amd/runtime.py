@@ -144,7 +144,7 @@ class StepPlan:
         self.gemm_ws = torch.empty(self._gemm_need, dtype=torch.float32, device=dev)
         attn_need = kernels.hip.size_call("cir_paged_attention_workspace_bytes", rows, rt.config.num_attention_heads,
                                           rt.config.head_dim, max_pages * rt.kv_allocator.page_size)
-        self.attn_ws = torch.empty(max(attn_need, 4), dtype=torch.uint8, device=dev)
+        self.attn_ws = torch.zeros(max(attn_need, 4), dtype=torch.uint8, device=dev)  # zeroed once; calls leave it zeroed
 
     # ------------------------------------------------------------------ build --
     def _build(self, graph: Graph) -> None:

@@ -35,6 +35,8 @@ def common_flags() -> list[str]:
         f"-I{ROOT / 'include'}", f"-I{SRC}",
         # Packed-FP32 VALU forms stay off in generated code (hardware notes).
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        # MFMA results in VGPRs (no accumulator-register copies before the scale FMAs).
+        "-mllvm", "-amdgpu-mfma-vgpr-form",
         "-Wno-unused-result",
     ]
 

@@ -1,23 +1,28 @@
 // Paged decode / prefill attention for gfx950.
 //
-// Work unit: one wavefront per (row, KV head, 128-token chunk of the context).
-// A row is one query token (batch * q_len rows); all GQA query heads of the KV
-// head are handled by the same wavefront, so each K/V page is read from HBM once.
+// A query row is one token (batch * q_len rows).  One workgroup handles one
+// (row, KV head, context split); all GQA query heads of the KV head are computed
+// together, so each K/V page is read from HBM once.  The host picks the number of
+// splits S: 1 whenever rows * kv_heads already fills the GPU (then the workgroup
+// writes the final output and nothing goes through global memory), otherwise a
+// few splits whose (max, sum, O) partials a small merge kernel combines.
 //
-// fp16 pools, head_dim 128 (Llama-3 / Qwen2 shapes):
+// fp16 pools, head_dim 128 (Llama-3 / Qwen2 shapes), 8 wavefronts per workgroup:
+//   * the split's context is cut into 64-token blocks dealt round-robin to the
+//     wavefronts; a wavefront issues every K and V load of its block up front
+//     (16 KiB of K and 16 KiB of V in flight, no branches: tiles past the end are
+//     clamped to a valid page and masked);
 //   * S = Q K^T on MFMA 16x16x32 f16: A = the group's query heads padded to 16
-//     rows, B = one 16-token tile of K read straight from the page (token rows of
-//     256 B, so a wavefront load covers 16 x 64 B); fp32 accumulate.
-//   * softmax is exact within the chunk (scores for the whole chunk stay in
-//     registers), in base 2 with scale*log2(e) folded into the scores.
-//   * O = P V on VALU: each lane owns 8 contiguous head dims of 4 token rows per
-//     tile (1 KiB contiguous per load instruction); P is fetched from the score
-//     lanes with ds_bpermute shuffles; the four token groups are summed once per
-//     chunk with cross-row shuffles.
-//   * The chunk's unnormalised O and its (max, sum) go to the workspace; a
-//     combine kernel merges the chunks with log-sum-exp weights.
-// fp32 pools (tiny-model parity path) use a plain VALU kernel with the same
-// workspace layout and the same combine kernel.
+//     rows, B = a 16-token tile of K read straight from its page (token rows of
+//     256 B); fp32 accumulate;
+//   * softmax in base 2 (scale*log2(e) folded into the scores): exact within the
+//     block, online (running max / rescale) across a wavefront's blocks;
+//   * O = P V on VALU: a lane owns 8 contiguous head dims of 4 token rows of each
+//     tile (1 KiB contiguous per load instruction); P comes from the score lanes by
+//     ds_bpermute shuffles; the four token groups are summed once at the end;
+//   * the 8 wavefronts merge (max, sum, O) through LDS with log-sum-exp weights.
+// fp32 pools and other head sizes (tiny-model parity path) use a plain VALU kernel
+// over 128-token chunks that always writes partials, merged by the same kernel.
 //
 // Reference semantics: cacheir/backends/triton_kernels.py:174-217 (paged gather
 // pool[page_table[b, t // P], kvh, t % P], GQA kvh = h // (Hq/Hkv), positions
@@ -30,8 +35,10 @@
 namespace cir {
 namespace {
 
-constexpr int kChunk = 128;          // context tokens per wavefront
-constexpr int kTiles = kChunk / 16;  // 16-token MFMA tiles per chunk
+constexpr int kBlock = 64;   // tokens per wavefront step (4 MFMA tiles of 16)
+constexpr int kWaves = 8;    // wavefronts per workgroup (fp16 path)
+constexpr int kChunk = 128;  // tokens per partial in the generic path
+constexpr int kMinSplitTokens = 256;
 constexpr float kLog2e = 1.4426950408889634f;
 
 // Tokens visible to query row `row`, clamped to what the page table can address.
@@ -41,167 +48,130 @@ __device__ __forceinline__ int visible_len(const int32_t* lens, int row, int q_l
   return min(lens[b] - q_len + s + 1, max_ctx);
 }
 
-// Merge the chunks of heads [head0, head0 + nh) of one row:
-// out = sum_c 2^(m_c - M) O_c / sum_c 2^(m_c - M) l_c.  One wavefront.
-template <typename T>
-__device__ void merge_chunks(const float* __restrict__ part_o, const float* __restrict__ part_ml, T* __restrict__ out,
-                             int row, int head0, int nh, int Hq, int D, int NC, int nc, int lane) {
-  for (int h = 0; h < nh; ++h) {
-    const int head = head0 + h;
-    const float* ml = part_ml + ((size_t)row * Hq + head) * NC * 2;
-    float M = -INFINITY;
-    for (int c = 0; c < nc; ++c) M = fmaxf(M, ml[2 * c]);
-    float denom = 0.f;
-    for (int c = 0; c < nc; ++c) denom += ml[2 * c + 1] * exp2f(ml[2 * c] - M);
-    const float inv = denom > 0.f ? 1.f / denom : 0.f;
-    const float* po = part_o + ((size_t)row * Hq + head) * NC * D;
-    for (int d = lane; d < D; d += 64) {
-      float o = 0.f;
-      for (int c = 0; c < nc; ++c) o = fmaf(po[(size_t)c * D + d], exp2f(ml[2 * c] - M), o);
-      out[((size_t)row * Hq + head) * D + d] = from_f32<T>(o * inv);
-    }
-  }
-}
-
-// Called by every wavefront after it stored its chunk.  The wavefront that takes the
-// last ticket of (row, kvh) merges all chunks and resets the counter to zero.
-template <typename T>
-__device__ void finish_chunk(const float* part_o, const float* part_ml, int* counters, T* out, int row, int kvh,
-                             int G, int Hq, int Hkv, int D, int NC, int L, int lane) {
-  __threadfence();  // publish this chunk's partials (agent-scope release)
-  int ticket = 0;
-  if (lane == 0) ticket = atomicAdd(&counters[(size_t)row * Hkv + kvh], 1);
-  ticket = __shfl(ticket, 0, 64);
-  const int nc = (L + kChunk - 1) / kChunk;
-  if (ticket != nc - 1) return;
-  __threadfence();  // acquire: see every other chunk's partials
-  merge_chunks<T>(part_o, part_ml, out, row, kvh * G, G, Hq, D, NC, nc, lane);
-  if (lane == 0) counters[(size_t)row * Hkv + kvh] = 0;
-}
-
-// A row with nothing visible (seq_len 0) gets zeros from its chunk-0 wavefront.
-template <typename T>
-__device__ void zero_heads(T* out, int row, int head0, int nh, int Hq, int D, int lane) {
-  for (int h = 0; h < nh; ++h)
-    for (int d = lane; d < D; d += 64) out[((size_t)row * Hq + head0 + h) * D + d] = from_f32<T>(0.f);
-}
-
 // ----------------------------------------------------------------------------
-// fp16 pools, head_dim 128, MFMA scores.  G = query heads per KV head (1..8).
+// fp16 pools, head_dim 128.  G = query heads per KV head (1..8).
 template <int G>
-__global__ __launch_bounds__(64) void attn_chunk_f16_d128(
+__global__ __launch_bounds__(64 * kWaves) void attn_f16_d128(
     const f16* __restrict__ q, const f16* __restrict__ kp, const f16* __restrict__ vp,
-    const int32_t* __restrict__ pt, const int32_t* __restrict__ lens,
-    float* __restrict__ part_o, float* __restrict__ part_ml, int* __restrict__ counters, f16* __restrict__ out,
-    int q_len, int Hq, int Hkv, int P, int max_pages, int NC, float scale_log2) {
+    const int32_t* __restrict__ pt, const int32_t* __restrict__ lens, f16* __restrict__ out,
+    float* __restrict__ part_o, float* __restrict__ part_ml, int q_len, int Hq, int Hkv, int P, int max_pages,
+    int S, float scale_log2) {
   constexpr int D = 128;
-  const int chunk = blockIdx.x, kvh = blockIdx.y, row = blockIdx.z;
-  const int L = visible_len(lens, row, q_len, max_pages * P);
-  const int t0 = chunk * kChunk;
-  if (t0 >= L) {
-    if (chunk == 0) zero_heads<f16>(out, row, kvh * G, G, Hq, D, threadIdx.x);
-    return;
-  }
-  const int t1 = min(L, t0 + kChunk);
-  const int b = row / q_len;
-  const int lane = threadIdx.x;
-  const int li = lane & 15;   // MFMA column (token within tile) / row of A
-  const int lg = lane >> 4;   // k-group
+  __shared__ float sm_m[kWaves][16];
+  __shared__ float sm_l[kWaves][16];
+  __shared__ float sm_o[kWaves][G][D];
 
-  // Q as the A operand: row li = query head (kvh*G + li) if li < G; element e of
-  // step s covers head dim 32*s + 8*lg + e (the same mapping K uses below).
-  f16x8 qa[4];
-  {
-    const f16* qrow = q + ((size_t)row * Hq + (size_t)kvh * G + li) * D + 8 * lg;
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      if (li < G) {
-        qa[s] = *reinterpret_cast<const f16x8*>(qrow + 32 * s);
-      } else {
-        qa[s] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
-      }
-    }
-  }
+  const int split = blockIdx.x, kvh = blockIdx.y, row = blockIdx.z;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int li = lane & 15;  // score column (token in tile) / Q row (head in group)
+  const int lg = lane >> 4;  // k-group of the MFMA operands; token group for P V
+  const int L = visible_len(lens, row, q_len, max_pages * P);
+  const int nblk = L > 0 ? (L + kBlock - 1) / kBlock : 0;
+  const int per = (nblk + S - 1) / S;
+  const int b0 = split * per, b1 = min(nblk, b0 + per);
+  const int b = row / q_len;
   const int32_t* ptrow = pt + (size_t)b * max_pages;
 
-  // Pass 1: scores.  sc[tile][r] = S[head 4*lg + r][token t0 + 16*tile + li].
-  f32x4 sc[kTiles];
+  // Q as the MFMA A operand: row li = head kvh*G + li (zero rows past G); element e
+  // of step s is head dim 32*s + 8*lg + e, the same mapping the K loads use.
+  f16x8 qa[4];
+  {
+    const f16* qrow = q + ((size_t)row * Hq + (size_t)kvh * G + (li < G ? li : 0)) * D + 8 * lg;
 #pragma unroll
-  for (int tile = 0; tile < kTiles; ++tile) {
-    const int tt = t0 + 16 * tile;
-    if (tt < t1) {
-      const int page = ptrow[tt / P];
-      const int off = tt - (tt / P) * P;
-      const f16* krow = kp + (((size_t)page * Hkv + kvh) * P + off + li) * D + 8 * lg;
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const f16x8 kb = *reinterpret_cast<const f16x8*>(krow + 32 * s);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[s], kb, acc, 0, 0, 0);
-      }
-      const bool valid = (tt + li) < t1;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) sc[tile][r] = valid ? acc[r] * scale_log2 : -INFINITY;
-    } else {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) sc[tile][r] = -INFINITY;
+    for (int s = 0; s < 4; ++s) {
+      const f16x8 v = *reinterpret_cast<const f16x8*>(qrow + 32 * s);
+      qa[s] = (li < G) ? v : f16x8{0, 0, 0, 0, 0, 0, 0, 0};
     }
   }
 
-  // Row max and sum per head (a row of 16 lanes shares the same 4 heads).
-  float m[4], l[4];
+  float m[4], lsum[4];
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    float mx = -INFINITY;
-#pragma unroll
-    for (int tile = 0; tile < kTiles; ++tile) mx = fmaxf(mx, sc[tile][r]);
-#pragma unroll
-    for (int off = 1; off < 16; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-    m[r] = mx;
-    float sum = 0.f;
-#pragma unroll
-    for (int tile = 0; tile < kTiles; ++tile) {
-      const float p = (sc[tile][r] == -INFINITY) ? 0.f : exp2f(sc[tile][r] - mx);
-      sc[tile][r] = p;
-      sum += p;
-    }
-#pragma unroll
-    for (int off = 1; off < 16; off <<= 1) sum += __shfl_xor(sum, off, 64);
-    l[r] = sum;
+    m[r] = -INFINITY;
+    lsum[r] = 0.f;
   }
-
-  // Pass 2: O = P V.  Lane owns dims 8*li..8*li+7 of tokens 4*u + lg of each tile.
   float acc[G][8];
 #pragma unroll
   for (int h = 0; h < G; ++h)
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[h][e] = 0.f;
 
+  for (int blk = b0 + wave; blk < b1; blk += kWaves) {
+    const int tb = blk * kBlock;
+    // Issue every K and V load of the block before using any of them.
+    f16x8 kb[4][4], vb[4][4];
 #pragma unroll
-  for (int tile = 0; tile < kTiles; ++tile) {
-    const int tt = t0 + 16 * tile;
-    if (tt < t1) {
-      const int page = ptrow[tt / P];
-      const int off = tt - (tt / P) * P;
-      const f16* vtile = vp + (((size_t)page * Hkv + kvh) * P + off) * D + 8 * li;
+    for (int j = 0; j < 4; ++j) {
+      const int tj = tb + 16 * j;
+      const int tv = tj < L ? tj : tb;  // tiles past the end re-read tile 0 (masked below)
+      const int page = ptrow[tv / P];
+      const size_t base = (((size_t)page * Hkv + kvh) * P + (tv % P)) * D;
+      const f16* krow = kp + base + (size_t)li * D + 8 * lg;
+      const f16* vrow = vp + base + 8 * li;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) kb[j][s] = *reinterpret_cast<const f16x8*>(krow + 32 * s);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) vb[j][u] = *reinterpret_cast<const f16x8*>(vrow + (size_t)(4 * u + lg) * D);
+    }
+    // Keep all 32 loads ahead of their first use (the scheduler would otherwise
+    // interleave them with the MFMAs and leave one 1 KiB load in flight).
+    __builtin_amdgcn_sched_barrier(0);
+    // Scores: sc[j][r] = S[head 4*lg + r][token tb + 16*j + li].
+    f32x4 sc[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      f32x4 c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < 4; ++s) c = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[s], kb[j][s], c, 0, 0, 0);
+      const bool valid = tb + 16 * j + li < L;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sc[j][r] = valid ? c[r] * scale_log2 : -INFINITY;
+    }
+    // Online softmax update per head row (the 16 lanes of a row share 4 heads).
+    float alpha[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float bm = fmaxf(fmaxf(sc[0][r], sc[1][r]), fmaxf(sc[2][r], sc[3][r]));
+#pragma unroll
+      for (int off = 1; off < 16; off <<= 1) bm = fmaxf(bm, __shfl_xor(bm, off, 64));
+      const float mn = fmaxf(m[r], bm);  // finite: token tb is always visible
+      alpha[r] = exp2f(m[r] - mn);
+      float ps = 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float p = exp2f(sc[j][r] - mn);
+        sc[j][r] = p;
+        ps += p;
+      }
+      lsum[r] = lsum[r] * alpha[r] + ps;
+      m[r] = mn;
+    }
+    // Rescale O, then O += P V.  Head h's alpha / p live in lanes 16*(h/4).., register h%4.
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      const float a = __shfl(alpha[h & 3], 16 * (h >> 2), 64);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[h][e] *= a;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const int tok = 4 * u + lg;
-        const f16x8 vv = *reinterpret_cast<const f16x8*>(vtile + (size_t)tok * D);
         float vf[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) vf[e] = static_cast<float>(vv[e]);
+        for (int e = 0; e < 8; ++e) vf[e] = static_cast<float>(vb[j][u][e]);
 #pragma unroll
         for (int h = 0; h < G; ++h) {
-          // p[h][tok] lives in lane tok + 16*(h/4), register h%4.
-          const float p = __shfl(sc[tile][h & 3], tok + 16 * (h >> 2), 64);
+          const float p = __shfl(sc[j][h & 3], tok + 16 * (h >> 2), 64);
 #pragma unroll
           for (int e = 0; e < 8; ++e) acc[h][e] = fmaf(p, vf[e], acc[h][e]);
         }
       }
     }
   }
-  // Sum the four token groups (lanes li, li+16, li+32, li+48).
+
+  // Wavefront totals: O over the 4 token groups, l over the 16 lanes of a row.
 #pragma unroll
   for (int h = 0; h < G; ++h)
 #pragma unroll
@@ -211,37 +181,63 @@ __global__ __launch_bounds__(64) void attn_chunk_f16_d128(
       v += __shfl_xor(v, 32, 64);
       acc[h][e] = v;
     }
-
-  if (lg == 0) {
 #pragma unroll
-    for (int h = 0; h < G; ++h) {
-      const int head = kvh * G + h;
-      float* dst = part_o + (((size_t)row * Hq + head) * NC + chunk) * D + 8 * li;
-      *reinterpret_cast<float4*>(dst) = make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
-      *reinterpret_cast<float4*>(dst + 4) = make_float4(acc[h][4], acc[h][5], acc[h][6], acc[h][7]);
-    }
-  }
+  for (int r = 0; r < 4; ++r)
+#pragma unroll
+    for (int off = 1; off < 16; off <<= 1) lsum[r] += __shfl_xor(lsum[r], off, 64);
+
   if (li == 0) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int h = 4 * lg + r;
-      if (h < G) {
-        float* ml = part_ml + (((size_t)row * Hq + kvh * G + h) * NC + chunk) * 2;
-        ml[0] = m[r];
-        ml[1] = l[r];
+      sm_m[wave][4 * lg + r] = m[r];
+      sm_l[wave][4 * lg + r] = lsum[r];
+    }
+  }
+  if (lg == 0) {
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sm_o[wave][h][8 * li + e] = acc[h][e];
+  }
+  __syncthreads();
+
+  // Merge the wavefronts: one thread per (head, dim).
+  for (int idx = threadIdx.x; idx < G * D; idx += 64 * kWaves) {
+    const int h = idx / D, d = idx - h * D;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, sm_m[w][h]);
+    float den = 0.f, o = 0.f;
+    if (M != -INFINITY) {
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) {
+        const float f = exp2f(sm_m[w][h] - M);
+        den = fmaf(sm_l[w][h], f, den);
+        o = fmaf(sm_o[w][h][d], f, o);
+      }
+    }
+    const int head = kvh * G + h;
+    if (S == 1) {
+      out[((size_t)row * Hq + head) * D + d] = static_cast<f16>(den > 0.f ? o / den : 0.f);
+    } else {
+      part_o[(((size_t)row * Hq + head) * S + split) * D + d] = o;
+      if (d == 0) {
+        float* ml = part_ml + (((size_t)row * Hq + head) * S + split) * 2;
+        ml[0] = M;
+        ml[1] = den;
       }
     }
   }
-  finish_chunk<f16>(part_o, part_ml, counters, out, row, kvh, G, Hq, Hkv, D, NC, L, lane);
 }
 
 // ----------------------------------------------------------------------------
-// Generic VALU kernel (fp32 or fp16 pools, any page size, head_dim <= 256).
+// Generic VALU kernel (fp32 or fp16 pools, any page size, head_dim <= 256):
+// one wavefront per (128-token chunk, KV head, row); always writes partials.
 template <typename T>
 __global__ __launch_bounds__(64) void attn_chunk_generic(
     const T* __restrict__ q, const T* __restrict__ kp, const T* __restrict__ vp,
     const int32_t* __restrict__ pt, const int32_t* __restrict__ lens,
-    float* __restrict__ part_o, float* __restrict__ part_ml, int* __restrict__ counters, T* __restrict__ out,
+    float* __restrict__ part_o, float* __restrict__ part_ml,
     int q_len, int Hq, int Hkv, int D, int P, int max_pages, int NC, float scale_log2) {
   __shared__ float qs[256];
   __shared__ float ps[kChunk];
@@ -250,15 +246,20 @@ __global__ __launch_bounds__(64) void attn_chunk_generic(
   const int t0 = chunk * kChunk;
   const int G = Hq / Hkv;
   const int lane = threadIdx.x;
-  if (t0 >= L) {
-    if (chunk == 0) zero_heads<T>(out, row, kvh * G, G, Hq, D, lane);
-    return;
-  }
-  const int n = min(L, t0 + kChunk) - t0;
+  const int n = max(0, min(L, t0 + kChunk) - t0);
   const int b = row / q_len;
   const int32_t* ptrow = pt + (size_t)b * max_pages;
   for (int h = 0; h < G; ++h) {
     const int head = kvh * G + h;
+    float* ml = part_ml + (((size_t)row * Hq + head) * NC + chunk) * 2;
+    if (n == 0) {  // empty chunk: neutral partial
+      for (int d = lane; d < D; d += 64) part_o[(((size_t)row * Hq + head) * NC + chunk) * D + d] = 0.f;
+      if (lane == 0) {
+        ml[0] = -INFINITY;
+        ml[1] = 0.f;
+      }
+      continue;
+    }
     __syncthreads();
     for (int d = lane; d < D; d += 64) qs[d] = to_f32(q[((size_t)row * Hq + head) * D + d]);
     __syncthreads();
@@ -292,15 +293,46 @@ __global__ __launch_bounds__(64) void attn_chunk_generic(
       part_o[(((size_t)row * Hq + head) * NC + chunk) * D + d] = o;
     }
     if (lane == 0) {
-      float* ml = part_ml + (((size_t)row * Hq + head) * NC + chunk) * 2;
       ml[0] = mx;
       ml[1] = sum;
     }
   }
-  finish_chunk<T>(part_o, part_ml, counters, out, row, kvh, G, Hq, Hkv, D, NC, L, lane);
 }
 
-int num_chunks(int max_context) { return max_context > 0 ? (max_context + kChunk - 1) / kChunk : 1; }
+// ----------------------------------------------------------------------------
+// Merge S partials of one (row, head): out = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s.
+template <typename T>
+__global__ __launch_bounds__(128) void attn_merge(const float* __restrict__ part_o, const float* __restrict__ part_ml,
+                                                  T* __restrict__ out, int Hq, int D, int S) {
+  const int head = blockIdx.x, row = blockIdx.y;
+  const float* ml = part_ml + ((size_t)row * Hq + head) * S * 2;
+  float M = -INFINITY;
+  for (int s = 0; s < S; ++s) M = fmaxf(M, ml[2 * s]);
+  float den = 0.f;
+  if (M != -INFINITY)
+    for (int s = 0; s < S; ++s) den = fmaf(ml[2 * s + 1], exp2f(ml[2 * s] - M), den);
+  const float inv = den > 0.f ? 1.f / den : 0.f;
+  const float* po = part_o + ((size_t)row * Hq + head) * S * D;
+  for (int d = threadIdx.x; d < D; d += blockDim.x) {
+    float o = 0.f;
+    if (M != -INFINITY)
+      for (int s = 0; s < S; ++s) o = fmaf(po[(size_t)s * D + d], exp2f(ml[2 * s] - M), o);
+    out[((size_t)row * Hq + head) * D + d] = from_f32<T>(o * inv);
+  }
+}
+
+int max_splits(int max_context) { return max(1, (max_context + kMinSplitTokens - 1) / kMinSplitTokens); }
+
+int generic_chunks(int max_context) { return max(1, (max_context + kChunk - 1) / kChunk); }
+
+// Splits for the fp16 path: 1 when rows*kv_heads workgroups of 8 wavefronts already
+// cover the 256 CUs; otherwise enough to reach about 320 workgroups.
+int choose_splits(int rows, int Hkv, int max_context) {
+  const long groups = (long)rows * Hkv;
+  if (groups >= 160) return 1;
+  const int want = (int)((320 + groups - 1) / groups);
+  return max(1, min(want, max_splits(max_context)));
+}
 
 int launch_attention(const void* q, const void* k_pool, const void* v_pool, const int32_t* page_table,
                      const int32_t* seq_lens, void* out, void* workspace, size_t workspace_bytes,
@@ -308,49 +340,60 @@ int launch_attention(const void* q, const void* k_pool, const void* v_pool, cons
                      int kv_dtype, void* stream) {
   CIR_CHECK_ARG(batch >= 0 && q_len >= 1, "attention: batch must be >= 0 and q_len >= 1");
   if (batch == 0) return 0;
-  CIR_CHECK_ARG(q && k_pool && v_pool && page_table && seq_lens && out && workspace, "attention: null pointer");
+  CIR_CHECK_ARG(q && k_pool && v_pool && page_table && seq_lens && out, "attention: null pointer");
   CIR_CHECK_ARG(Hkv > 0 && Hq > 0 && Hq % Hkv == 0, "attention: num_heads (%d) must be a multiple of num_kv_heads (%d)", Hq, Hkv);
   CIR_CHECK_ARG(D > 0 && D <= 256, "attention: head_dim %d out of range (1..256)", D);
   CIR_CHECK_ARG(P > 0 && max_pages > 0, "attention: page_size and max_pages must be positive");
   CIR_CHECK_ARG(kv_dtype == CIR_F16 || kv_dtype == CIR_F32, "attention: kv_dtype must be CIR_F16 or CIR_F32");
   const int rows = batch * q_len;
-  const int NC = num_chunks(max_pages * P);
-  const size_t need = cir_paged_attention_workspace_bytes(rows, Hq, D, max_pages * P);
-  CIR_CHECK_ARG(workspace_bytes >= need, "attention: workspace too small (%zu < %zu)", workspace_bytes, need);
+  const int max_ctx = max_pages * P;
   CIR_CHECK_ARG(rows <= 65535 && Hkv <= 65535, "attention: grid too large");
-  float* part_o = static_cast<float*>(workspace);
-  float* part_ml = part_o + (size_t)rows * Hq * NC * D;
-  int* counters = reinterpret_cast<int*>(part_ml + (size_t)rows * Hq * NC * 2);
+  const size_t need = cir_paged_attention_workspace_bytes(rows, Hq, D, max_ctx);
+  CIR_CHECK_ARG(workspace && workspace_bytes >= need, "attention: workspace too small (%zu < %zu)", workspace_bytes,
+                need);
   const float scale_log2 = scale * kLog2e;
   const int G = Hq / Hkv;
   hipStream_t s = as_stream(stream);
-  dim3 grid(NC, Hkv, rows);
   const bool mfma = kv_dtype == CIR_F16 && D == 128 && P % 16 == 0 && G <= 8;
+  const int S = mfma ? choose_splits(rows, Hkv, max_ctx) : generic_chunks(max_ctx);
+  float* part_o = static_cast<float*>(workspace);
+  float* part_ml = part_o + (size_t)rows * Hq * S * D;
+  dim3 grid(S, Hkv, rows);
   if (mfma) {
     auto kq = static_cast<const f16*>(q);
     auto kk = static_cast<const f16*>(k_pool);
     auto kv = static_cast<const f16*>(v_pool);
-#define CIR_ATT_CASE(g)                                                                                    \
-  case g:                                                                                                  \
-    attn_chunk_f16_d128<g><<<grid, 64, 0, s>>>(kq, kk, kv, page_table, seq_lens, part_o, part_ml, counters,   \
-                                               static_cast<f16*>(out), q_len, Hq, Hkv, P, max_pages, NC,  \
-                                               scale_log2);                                                \
+    auto ko = static_cast<f16*>(out);
+#define CIR_ATT_CASE(g)                                                                                             \
+  case g:                                                                                                           \
+    attn_f16_d128<g><<<grid, 64 * kWaves, 0, s>>>(kq, kk, kv, page_table, seq_lens, ko, part_o, part_ml, q_len, Hq, \
+                                                  Hkv, P, max_pages, S, scale_log2);                                \
     break;
     switch (G) {
       CIR_ATT_CASE(1) CIR_ATT_CASE(2) CIR_ATT_CASE(3) CIR_ATT_CASE(4)
       CIR_ATT_CASE(5) CIR_ATT_CASE(6) CIR_ATT_CASE(7) CIR_ATT_CASE(8)
     }
 #undef CIR_ATT_CASE
-  } else if (kv_dtype == CIR_F16) {
-    attn_chunk_generic<f16><<<grid, 64, 0, s>>>(static_cast<const f16*>(q), static_cast<const f16*>(k_pool),
-                                                static_cast<const f16*>(v_pool), page_table, seq_lens, part_o,
-                                                part_ml, counters, static_cast<f16*>(out), q_len, Hq, Hkv, D, P,
-                                                max_pages, NC, scale_log2);
+    const int st = launch_status();
+    if (st || S == 1) return st;
   } else {
-    attn_chunk_generic<float><<<grid, 64, 0, s>>>(static_cast<const float*>(q), static_cast<const float*>(k_pool),
-                                                  static_cast<const float*>(v_pool), page_table, seq_lens, part_o,
-                                                  part_ml, counters, static_cast<float*>(out), q_len, Hq, Hkv, D, P,
-                                                  max_pages, NC, scale_log2);
+    if (kv_dtype == CIR_F16) {
+      attn_chunk_generic<f16><<<grid, 64, 0, s>>>(static_cast<const f16*>(q), static_cast<const f16*>(k_pool),
+                                                  static_cast<const f16*>(v_pool), page_table, seq_lens, part_o,
+                                                  part_ml, q_len, Hq, Hkv, D, P, max_pages, S, scale_log2);
+    } else {
+      attn_chunk_generic<float><<<grid, 64, 0, s>>>(static_cast<const float*>(q), static_cast<const float*>(k_pool),
+                                                    static_cast<const float*>(v_pool), page_table, seq_lens, part_o,
+                                                    part_ml, q_len, Hq, Hkv, D, P, max_pages, S, scale_log2);
+    }
+    const int st = launch_status();
+    if (st) return st;
+  }
+  dim3 mgrid(Hq, rows);
+  if (kv_dtype == CIR_F16) {
+    attn_merge<f16><<<mgrid, 128, 0, s>>>(part_o, part_ml, static_cast<f16*>(out), Hq, D, S);
+  } else {
+    attn_merge<float><<<mgrid, 128, 0, s>>>(part_o, part_ml, static_cast<float*>(out), Hq, D, S);
   }
   return launch_status();
 }
@@ -360,9 +403,10 @@ int launch_attention(const void* q, const void* k_pool, const void* v_pool, cons
 
 extern "C" size_t cir_paged_attention_workspace_bytes(int rows, int num_heads, int head_dim, int max_context) {
   if (rows <= 0 || num_heads <= 0 || head_dim <= 0) return 0;
-  const size_t nc = (size_t)cir::num_chunks(max_context);
-  // partial O and (max, sum) per (row, head, chunk), then one ticket counter per (row, head)
-  return (size_t)rows * num_heads * nc * ((size_t)head_dim + 2) * sizeof(float) + (size_t)rows * num_heads * sizeof(int);
+  // Partial O and (max, sum) per (row, head, split), sized for the larger split count of the two paths.
+  const int a = cir::max_splits(max_context), c = cir::generic_chunks(max_context);
+  const size_t s = (size_t)(a > c ? a : c);
+  return (size_t)rows * num_heads * s * ((size_t)head_dim + 2) * sizeof(float);
 }
 
 extern "C" int cir_paged_decode_attention(const void* q, const void* k_pool, const void* v_pool,

@@ -24,7 +24,9 @@
 //   one 32-value block, so its fp32 result is scaled by the block's d in fp32 and
 //   added to the accumulator.  Products and the scale are exact in fp32, so the
 //   only deviation from the fp32 reference (dequant then matmul, cpu.py:306-312)
-//   is fp32 summation order.
+//   is fp32 summation order.  (Rounding the weights to fp16 instead, as the
+//   reference CUDA path does at cuda.py:935, misses the 2e-3 + 1e-2|y| bound at
+//   k = 14336.)
 //
 // GEMM: workgroup = 4 wavefronts on the same NT*16 output rows; the wavefronts
 // interleave over the quads of the workgroup's k-range and their fp32 accumulators
@@ -35,7 +37,12 @@
 namespace cir {
 namespace {
 
-__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t c) { return (a & m) | c; }
+// (a & m) | c in one v_and_or_b32 (the compiler otherwise emits v_and + v_or with literals).
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t c) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(m), "v"(c));
+  return r;
+}
 
 __device__ __forceinline__ f16x2 as_h2(uint32_t v) { return __builtin_bit_cast(f16x2, v); }
 
@@ -175,22 +182,86 @@ __global__ void dequant_tiled_kernel(const uint8_t* __restrict__ q, const uint16
 }
 
 // ------------------------------------------------------------------ GEMM -----
+// One quad (128 columns) of operands for one wavefront: NT weight tiles and MT x tiles.
+template <int FMT, int NT, int MT>
+struct Stage {
+  static constexpr int LB = (FMT == CIR_Q4_0) ? 1 : 2;  // 16-byte loads per lane per weight tile
+  uint4 w[NT][LB];
+  uint2 d[NT];
+  f16x8 x[MT][4];
+};
+
+// wbase[b] / dbase[b] point at tile (nt0 + b, quad 0) for this lane; quads are
+// consecutive tiles, so quad Q is Q tile-strides further.
+template <int FMT, int NT, int MT>
+__device__ __forceinline__ void load_stage(Stage<FMT, NT, MT>& st, const uint4* const (&wbase)[NT],
+                                           const uint2* const (&dbase)[NT], const f16* const (&xrow)[MT], int Q) {
+  constexpr int LB = Stage<FMT, NT, MT>::LB;
+#pragma unroll
+  for (int b = 0; b < NT; ++b) {
+    const uint4* src = wbase[b] + (size_t)Q * (64 * LB);
+#pragma unroll
+    for (int c = 0; c < LB; ++c) st.w[b][c] = src[c];
+    st.d[b] = dbase[b][(size_t)Q * 16];
+  }
+#pragma unroll
+  for (int a = 0; a < MT; ++a)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) st.x[a][j] = *reinterpret_cast<const f16x8*>(xrow[a] + 128 * Q + 32 * j);
+}
+
+// Exact integer weights ((q - 8) for Q4_0, q for Q8_0) feed one MFMA per 32-value
+// block; the block's fp32 result is scaled by d in fp32 and accumulated.  All MFMAs
+// of a block step are issued before their scale FMAs so the MFMA latency overlaps.
+template <int FMT, int NT, int MT>
+__device__ __forceinline__ void compute_stage(const Stage<FMT, NT, MT>& st, f32x4 (&acc)[MT][NT]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    f32x4 c[MT][NT];
+    float dj[NT];
+#pragma unroll
+    for (int b = 0; b < NT; ++b) {
+      f16x8 wb;
+      if constexpr (FMT == CIR_Q4_0) {
+        const uint4 v = st.w[b][0];
+        wb = dq_q4((j == 0) ? v.x : (j == 1) ? v.y : (j == 2) ? v.z : v.w);
+      } else {
+        const uint4 v = st.w[b][j >> 1];
+        wb = dq_q8((j & 1) ? v.z : v.x, (j & 1) ? v.w : v.y);
+      }
+      const uint32_t dw = (j < 2) ? st.d[b].x : st.d[b].y;
+      dj[b] = static_cast<float>(__builtin_bit_cast(f16, (uint16_t)((j & 1) ? (dw >> 16) : (dw & 0xFFFFu))));
+#pragma unroll
+      for (int a = 0; a < MT; ++a)
+        c[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(st.x[a][j], wb, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+    }
+#pragma unroll
+    for (int b = 0; b < NT; ++b)
+#pragma unroll
+      for (int a = 0; a < MT; ++a)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[a][b][r] = fmaf(dj[b], c[a][b][r], acc[a][b][r]);
+  }
+}
+
 // FMT: CIR_Q4_0 or CIR_Q8_0.  NT: 16-row n-tiles per wavefront.  MT: 16-row m-tiles.
+// The four wavefronts of a workgroup take every fourth quad of the split; each
+// wavefront prefetches its next quad while it computes the current one.
 template <int FMT, int NT, int MT>
 __global__ __launch_bounds__(256) void qgemm_kernel(const f16* __restrict__ x, int ldx, const uint8_t* __restrict__ wq,
                                                     const uint16_t* __restrict__ wd, float* __restrict__ part, int M,
                                                     int N, int K, int quads_per_split) {
-  constexpr int LANE_BYTES = (FMT == CIR_Q4_0) ? 16 : 32;
   __shared__ f32x4 red[3][MT * NT][64];
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  constexpr int LB = Stage<FMT, NT, MT>::LB;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: keeps the quad loop scalar
+  const int lane = threadIdx.x & 63;
   const int li = lane & 15, lg = lane >> 4;
   const int KQ = K / 128;
   const int NTILES = (N + 15) / 16;
   const int nt0 = blockIdx.x * NT;
   const int split = blockIdx.y;
   const int m0 = blockIdx.z * 16 * MT;
-  const int qb = split * quads_per_split;
-  const int qe = qb + quads_per_split;
+  const int qe = split * quads_per_split + quads_per_split;
 
   f32x4 acc[MT][NT];
 #pragma unroll
@@ -198,64 +269,30 @@ __global__ __launch_bounds__(256) void qgemm_kernel(const f16* __restrict__ x, i
 #pragma unroll
     for (int b = 0; b < NT; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  // Rows past M read row M-1 (valid memory); their results are never stored.
   const f16* xrow[MT];
-  bool mvalid[MT];
 #pragma unroll
-  for (int a = 0; a < MT; ++a) {
-    const int m = m0 + 16 * a + li;
-    mvalid[a] = m < M;
-    xrow[a] = x + (size_t)(mvalid[a] ? m : 0) * ldx + 8 * lg;
+  for (int a = 0; a < MT; ++a) xrow[a] = x + (size_t)min(m0 + 16 * a + li, M - 1) * ldx + 8 * lg;
+  const uint4* wbase[NT];
+  const uint2* dbase[NT];
+#pragma unroll
+  for (int b = 0; b < NT; ++b) {
+    const size_t tile0 = (size_t)min(nt0 + b, NTILES - 1) * KQ;  // tiles past N re-read the last tile
+    wbase[b] = reinterpret_cast<const uint4*>(wq) + (tile0 * 64 + lane) * LB;
+    dbase[b] = reinterpret_cast<const uint2*>(wd) + tile0 * 16 + li;
   }
 
-  for (int Q = qb + wave; Q < qe; Q += 4) {
-    uint4 wv[NT][LANE_BYTES / 16];
-    uint2 dv[NT];
-#pragma unroll
-    for (int b = 0; b < NT; ++b) {
-      const int ntile = min(nt0 + b, NTILES - 1);
-      const size_t tile = (size_t)ntile * KQ + Q;
-      const uint4* src = reinterpret_cast<const uint4*>(wq + (tile * 64 + lane) * LANE_BYTES);
-#pragma unroll
-      for (int c = 0; c < LANE_BYTES / 16; ++c) wv[b][c] = src[c];
-      dv[b] = reinterpret_cast<const uint2*>(wd)[tile * 16 + li];
-    }
-    f16x8 xa[MT][4];
-#pragma unroll
-    for (int a = 0; a < MT; ++a)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        if (mvalid[a]) {
-          xa[a][j] = *reinterpret_cast<const f16x8*>(xrow[a] + 128 * Q + 32 * j);
-        } else {
-          xa[a][j] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
-        }
-      }
-#pragma unroll
-    for (int b = 0; b < NT; ++b) {
-      const float d4[4] = {static_cast<float>(__builtin_bit_cast(f16, (uint16_t)(dv[b].x & 0xFFFFu))),
-                           static_cast<float>(__builtin_bit_cast(f16, (uint16_t)(dv[b].x >> 16))),
-                           static_cast<float>(__builtin_bit_cast(f16, (uint16_t)(dv[b].y & 0xFFFFu))),
-                           static_cast<float>(__builtin_bit_cast(f16, (uint16_t)(dv[b].y >> 16)))};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        f16x8 wb;
-        if constexpr (FMT == CIR_Q4_0) {
-          const uint32_t w = (j == 0) ? wv[b][0].x : (j == 1) ? wv[b][0].y : (j == 2) ? wv[b][0].z : wv[b][0].w;
-          wb = dq_q4(w);
-        } else {
-          const uint4 v = wv[b][j >> 1];
-          const uint32_t w0 = (j & 1) ? v.z : v.x;
-          const uint32_t w1 = (j & 1) ? v.w : v.y;
-          wb = dq_q8(w0, w1);
-        }
-#pragma unroll
-        for (int a = 0; a < MT; ++a) {
-          const f32x4 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[a][j], wb, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-#pragma unroll
-          for (int r = 0; r < 4; ++r) acc[a][b][r] = fmaf(d4[j], c[r], acc[a][b][r]);
-        }
-      }
-    }
+  Stage<FMT, NT, MT> s0, s1;
+  int Q = split * quads_per_split + wave;
+  if (Q < qe) load_stage(s0, wbase, dbase, xrow, Q);
+  while (Q < qe) {
+    if (Q + 4 < qe) load_stage(s1, wbase, dbase, xrow, Q + 4);
+    compute_stage(s0, acc);
+    Q += 4;
+    if (Q >= qe) break;
+    if (Q + 4 < qe) load_stage(s0, wbase, dbase, xrow, Q + 4);
+    compute_stage(s1, acc);
+    Q += 4;
   }
 
   // Sum the four wavefronts' accumulators through LDS; wavefront 0 writes.
@@ -313,13 +350,19 @@ void launch_qgemm(const f16* x, int ldx, const uint8_t* wq, const uint16_t* wd, 
   qgemm_kernel<FMT, NT, MT><<<grid, 256, 0, s>>>(x, ldx, wq, wd, part, M, N, K, (K / 128) / splits);
 }
 
+// NT = 4 (64 rows per workgroup, best x reuse) unless that leaves fewer than ~256
+// workgroups, then NT = 2.
 template <int FMT>
 void dispatch_qgemm(const f16* x, int ldx, const uint8_t* wq, const uint16_t* wd, float* part, int M, int N, int K,
                     int splits, hipStream_t s) {
+  const long groups4 = (long)((N + 63) / 64) * splits * ((M + 31) / 32);
+  const bool wide = groups4 >= 256;
   if (M <= 16) {
-    launch_qgemm<FMT, 4, 1>(x, ldx, wq, wd, part, M, N, K, splits, s);
+    if (wide) launch_qgemm<FMT, 4, 1>(x, ldx, wq, wd, part, M, N, K, splits, s);
+    else launch_qgemm<FMT, 2, 1>(x, ldx, wq, wd, part, M, N, K, splits, s);
   } else {
-    launch_qgemm<FMT, 4, 2>(x, ldx, wq, wd, part, M, N, K, splits, s);
+    if (wide) launch_qgemm<FMT, 4, 2>(x, ldx, wq, wd, part, M, N, K, splits, s);
+    else launch_qgemm<FMT, 2, 2>(x, ldx, wq, wd, part, M, N, K, splits, s);
   }
 }
 

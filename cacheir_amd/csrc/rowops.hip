@@ -37,24 +37,79 @@ __global__ void embedding_kernel(const int64_t* __restrict__ ids, const TT* __re
 }
 
 // ---------------------------------------------------------------- rmsnorm ----
+constexpr int kRowThreads = 1024;
+constexpr int kRowVals = 8;  // rows up to 8192 stay in registers
+
+// Block-wide sum over 1024 threads (16 wavefronts).
+__device__ __forceinline__ float block_sum_1024(float v, float* scratch) {
+  v = wave_sum(v);
+  if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float t = 0.f;
+#pragma unroll
+  for (int w = 0; w < kRowThreads / 64; ++w) t += scratch[w];
+  return t;
+}
+
 template <typename TX, typename TW, typename TO>
-__global__ __launch_bounds__(256) void rmsnorm_kernel(const TX* __restrict__ x, const TW* __restrict__ w,
-                                                      TO* __restrict__ out, int hidden, float eps) {
-  __shared__ float partial[4];
+__global__ __launch_bounds__(kRowThreads) void rmsnorm_kernel(const TX* __restrict__ x, const TW* __restrict__ w,
+                                                              TO* __restrict__ out, int hidden, float eps) {
+  __shared__ float scratch[kRowThreads / 64];
   const int r = blockIdx.x;
   const TX* xr = x + (size_t)r * hidden;
+  float v[kRowVals];
   float ss = 0.f;
-  for (int i = threadIdx.x; i < hidden; i += 256) {
-    const float v = to_f32(xr[i]);
-    ss = fmaf(v, v, ss);
+#pragma unroll
+  for (int i = 0; i < kRowVals; ++i) {
+    const int c = threadIdx.x + i * kRowThreads;
+    v[i] = c < hidden ? to_f32(xr[c]) : 0.f;
+    ss = fmaf(v[i], v[i], ss);
   }
-  ss = wave_sum(ss);
-  if ((threadIdx.x & 63) == 0) partial[threadIdx.x >> 6] = ss;
-  __syncthreads();
-  const float total = partial[0] + partial[1] + partial[2] + partial[3];
-  const float scale = 1.0f / sqrtf(total / (float)hidden + eps);
+  for (int c = threadIdx.x + kRowVals * kRowThreads; c < hidden; c += kRowThreads) {
+    const float t = to_f32(xr[c]);
+    ss = fmaf(t, t, ss);
+  }
+  const float scale = 1.0f / sqrtf(block_sum_1024(ss, scratch) / (float)hidden + eps);
   TO* o = out + (size_t)r * hidden;
-  for (int i = threadIdx.x; i < hidden; i += 256) o[i] = from_f32<TO>((to_f32(xr[i]) * scale) * to_f32(w[i]));
+#pragma unroll
+  for (int i = 0; i < kRowVals; ++i) {
+    const int c = threadIdx.x + i * kRowThreads;
+    if (c < hidden) o[c] = from_f32<TO>((v[i] * scale) * to_f32(w[c]));
+  }
+  for (int c = threadIdx.x + kRowVals * kRowThreads; c < hidden; c += kRowThreads)
+    o[c] = from_f32<TO>((to_f32(xr[c]) * scale) * to_f32(w[c]));
+}
+
+// Residual epilogue + RMSNorm of the result, one workgroup per row:
+// h = residual + sum_s partial_s (fp32, written to h_out) and xn = (h * rsqrt(mean(h^2)+eps)) * w.
+template <typename TW, typename TO>
+__global__ __launch_bounds__(kRowThreads) void residual_rmsnorm_kernel(
+    const float* __restrict__ part, int splits, const float* __restrict__ resid, float* __restrict__ h_out,
+    const TW* __restrict__ w, TO* __restrict__ xn, int M, int N, float eps) {
+  __shared__ float scratch[kRowThreads / 64];
+  const int r = blockIdx.x;
+  const size_t plane = (size_t)M * N;
+  float v[kRowVals];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < kRowVals; ++i) {
+    const int c = threadIdx.x + i * kRowThreads;
+    float t = 0.f;
+    if (c < N) {
+      const size_t idx = (size_t)r * N + c;
+      t = resid[idx];
+      for (int sp = 0; sp < splits; ++sp) t += part[sp * plane + idx];
+      h_out[idx] = t;
+    }
+    v[i] = t;
+    ss = fmaf(t, t, ss);
+  }
+  const float scale = 1.0f / sqrtf(block_sum_1024(ss, scratch) / (float)N + eps);
+#pragma unroll
+  for (int i = 0; i < kRowVals; ++i) {
+    const int c = threadIdx.x + i * kRowThreads;
+    if (c < N) xn[(size_t)r * N + c] = from_f32<TO>((v[i] * scale) * to_f32(w[c]));
+  }
 }
 
 template <typename T>
@@ -149,36 +204,47 @@ __global__ void epi_qkv_kernel(const float* __restrict__ part, int splits, const
 }
 
 // ---------------------------------------------------------------- argmax -----
-__global__ __launch_bounds__(256) void argmax_kernel(const float* __restrict__ logits, int ld, int64_t* __restrict__ ids,
-                                                     int vocab) {
-  __shared__ float sv[256];
-  __shared__ int si[256];
+__device__ __forceinline__ void better(float& bv, int& bi, float v, int i) {
+  if (v > bv || (v == bv && i < bi)) {
+    bv = v;
+    bi = i;
+  }
+}
+
+__global__ __launch_bounds__(kRowThreads) void argmax_kernel(const float* __restrict__ logits, int ld,
+                                                             int64_t* __restrict__ ids, int vocab) {
+  __shared__ float sv[kRowThreads / 64];
+  __shared__ int si[kRowThreads / 64];
   const int r = blockIdx.x;
   const float* row = logits + (size_t)r * ld;
-  float best = -INFINITY;
+  float bv = -INFINITY;
   int bi = 0x7fffffff;
-  for (int i = threadIdx.x; i < vocab; i += 256) {
-    const float v = row[i];
-    if (v > best || (v == best && i < bi)) {
-      best = v;
-      bi = i;
-    }
+  constexpr int U = 4;
+  int base = threadIdx.x;
+  for (; base + (U - 1) * kRowThreads < vocab; base += U * kRowThreads) {
+    float t[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) t[u] = row[base + u * kRowThreads];
+#pragma unroll
+    for (int u = 0; u < U; ++u) better(bv, bi, t[u], base + u * kRowThreads);
   }
-  sv[threadIdx.x] = best;
-  si[threadIdx.x] = bi;
+  for (int i = base; i < vocab; i += kRowThreads) better(bv, bi, row[i], i);
+  // wavefront then workgroup reduction, ties to the smaller index
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const float ov = __shfl_xor(bv, off, 64);
+    const int oi = __shfl_xor(bi, off, 64);
+    better(bv, bi, ov, oi);
+  }
+  if ((threadIdx.x & 63) == 0) {
+    sv[threadIdx.x >> 6] = bv;
+    si[threadIdx.x >> 6] = bi;
+  }
   __syncthreads();
-  for (int stride = 128; stride > 0; stride >>= 1) {
-    if (threadIdx.x < stride) {
-      const float ov = sv[threadIdx.x + stride];
-      const int oi = si[threadIdx.x + stride];
-      if (ov > sv[threadIdx.x] || (ov == sv[threadIdx.x] && oi < si[threadIdx.x])) {
-        sv[threadIdx.x] = ov;
-        si[threadIdx.x] = oi;
-      }
-    }
-    __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < kRowThreads / 64; ++w) better(bv, bi, sv[w], si[w]);
+    ids[r] = bi == 0x7fffffff ? 0 : bi;
   }
-  if (threadIdx.x == 0) ids[r] = si[0] == 0x7fffffff ? 0 : si[0];
 }
 
 unsigned blocks_for(size_t n, unsigned bs) { return (unsigned)((n + bs - 1) / bs); }
@@ -218,7 +284,7 @@ extern "C" int cir_rmsnorm(const void* x, int xdt, const void* w, int wdt, void*
   CIR_CHECK_ARG(x && w && out, "rmsnorm: null pointer");
   hipStream_t s = as_stream(stream);
 #define CIR_RMS(TX, TW, TO) \
-  rmsnorm_kernel<TX, TW, TO><<<rows, 256, 0, s>>>((const TX*)x, (const TW*)w, (TO*)out, hidden, eps)
+  rmsnorm_kernel<TX, TW, TO><<<rows, kRowThreads, 0, s>>>((const TX*)x, (const TW*)w, (TO*)out, hidden, eps)
   const int key = xdt * 4 + wdt * 2 + odt;
   switch (key) {
     case 0: CIR_RMS(float, float, float); break;
@@ -273,6 +339,24 @@ extern "C" int cir_epilogue_store(const float* y_partial, int splits, const void
   return launch_status();
 }
 
+extern "C" int cir_epilogue_residual_rmsnorm(const float* y_partial, int splits, const float* residual, float* h_out,
+                                             const void* norm_w, int wdt, float eps, void* xn, int xdt, int m, int n,
+                                             void* stream) {
+  CIR_CHECK_ARG(valid_dt(wdt) && valid_dt(xdt) && splits >= 1 && m >= 0 && n >= 0, "epilogue_residual_rmsnorm: bad arguments");
+  if (m == 0 || n == 0) return 0;
+  CIR_CHECK_ARG(n <= kRowVals * kRowThreads, "epilogue_residual_rmsnorm: row length %d > %d", n, kRowVals * kRowThreads);
+  CIR_CHECK_ARG(y_partial && residual && h_out && norm_w && xn, "epilogue_residual_rmsnorm: null pointer");
+  hipStream_t s = as_stream(stream);
+#define CIR_RR(TW, TO) \
+  residual_rmsnorm_kernel<TW, TO><<<m, kRowThreads, 0, s>>>(y_partial, splits, residual, h_out, (const TW*)norm_w, (TO*)xn, m, n, eps)
+  if (wdt == CIR_F32 && xdt == CIR_F32) CIR_RR(float, float);
+  else if (wdt == CIR_F32 && xdt == CIR_F16) CIR_RR(float, f16);
+  else if (wdt == CIR_F16 && xdt == CIR_F32) CIR_RR(f16, float);
+  else CIR_RR(f16, f16);
+#undef CIR_RR
+  return launch_status();
+}
+
 extern "C" int cir_epilogue_swiglu(const float* y_partial, int splits, void* out, int odt, int m, int inter, void* stream) {
   CIR_CHECK_ARG(valid_dt(odt) && splits >= 1 && m >= 0 && inter >= 0, "epilogue_swiglu: bad arguments");
   if (m == 0 || inter == 0) return 0;
@@ -317,6 +401,6 @@ extern "C" int cir_argmax(const float* logits, int ld, int64_t* ids, int rows, i
   CIR_CHECK_ARG(rows >= 0 && vocab > 0 && ld >= vocab, "argmax: bad sizes");
   if (rows == 0) return 0;
   CIR_CHECK_ARG(logits && ids, "argmax: null pointer");
-  argmax_kernel<<<rows, 256, 0, as_stream(stream)>>>(logits, ld, ids, vocab);
+  argmax_kernel<<<rows, kRowThreads, 0, as_stream(stream)>>>(logits, ld, ids, vocab);
   return launch_status();
 }

@@ -39,6 +39,8 @@ _SIGNATURES = {
     "cir_qgemm": (_c_int, [_vp, _c_int, _vp, _c_int, _vp, _c_int, _c_int, _c_int, _c_int, _vp]),
     "cir_gemm_f32": (_c_int, [_vp, _c_int, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp]),
     "cir_epilogue_store": (_c_int, [_vp, _c_int, _vp, _vp, _c_int, _c_int, _c_int, _vp]),
+    "cir_epilogue_residual_rmsnorm": (_c_int, [_vp, _c_int, _vp, _vp, _vp, _c_int, _c_float, _vp, _c_int, _c_int,
+                                               _c_int, _vp]),
     "cir_epilogue_swiglu": (_c_int, [_vp, _c_int, _vp, _c_int, _c_int, _c_int, _vp]),
     "cir_epilogue_qkv_rope_append": (_c_int, [_vp, _c_int, _vp, _vp, _vp, _c_int, _vp, _c_int, _vp, _vp, _c_int, _c_int,
                                               _c_int, _c_int, _c_int, _c_int, _c_int, _vp]),

@@ -190,6 +190,21 @@ def epilogue_store(part: torch.Tensor, out_dtype: torch.dtype, residual: torch.T
     return out
 
 
+def epilogue_residual_rmsnorm(part: torch.Tensor, residual: torch.Tensor, norm_w: torch.Tensor, eps: float,
+                              h_out: torch.Tensor, xn_out: torch.Tensor):
+    """h_out = residual + sum(part) (fp32); xn_out = RMSNorm(h_out) * norm_w (GEMM input dtype)."""
+    splits, m, n = part.shape
+    for t, nm in ((residual, "residual"), (h_out, "h_out"), (xn_out, "xn_out"), (norm_w, "norm_w")):
+        _cuda(t, nm)
+    _req(residual.dtype == torch.float32 and h_out.dtype == torch.float32, "residual/h_out must be float32", TypeError)
+    _req(residual.numel() == m * n and h_out.numel() == m * n and xn_out.numel() == m * n and norm_w.numel() == n,
+         "residual_rmsnorm shape mismatch")
+    hip.call("cir_epilogue_residual_rmsnorm", part.data_ptr(), splits, residual.data_ptr(), h_out.data_ptr(),
+             norm_w.data_ptr(), hip.dtype_code(norm_w.dtype), float(eps), xn_out.data_ptr(),
+             hip.dtype_code(xn_out.dtype), m, n, hip.stream_handle())
+    return h_out, xn_out
+
+
 def epilogue_swiglu(part: torch.Tensor, out_dtype: torch.dtype, out=None):
     splits, m, n2 = part.shape
     _req(n2 % 2 == 0, "swiglu partials need gate|up columns")

@@ -152,7 +152,7 @@ class StepPlan:
         consumers = graph.consumers()
         env: dict[str, Any] = {}
         skip: set[int] = set()
-        appended: set[int] = set()
+        normed: dict[tuple[str, str], torch.Tensor] = {}  # (value, norm weight) -> RMSNorm already computed
         self.logits_name = graph.outputs[0]
 
         def gemm_dtype(weight) -> torch.dtype:
@@ -209,11 +209,13 @@ class StepPlan:
             elif op in _QKV_OPS:
                 layer = int(attrs.get("layer", 0))
                 x = env[ins[0]]
-                w_norm = rt.weights.dense(ins[1], rt.dense_dtype)
                 W = rt.weights.matmul_weight(tuple(ins[2:5]))
-                xn = buf(x.shape[1], gemm_dtype(W))
-                eps = float(attrs.get("eps", 1e-6))
-                self.launches.append(lambda x=x, w=w_norm, o=xn, e=eps: kernels.rmsnorm(x, w, e, o.dtype, out=o))
+                xn = normed.get((ins[0], ins[1]))
+                if xn is None or xn.dtype != gemm_dtype(W):
+                    w_norm = rt.weights.dense(ins[1], rt.dense_dtype)
+                    xn = buf(x.shape[1], gemm_dtype(W))
+                    eps = float(attrs.get("eps", 1e-6))
+                    self.launches.append(lambda x=x, w=w_norm, o=xn, e=eps: kernels.rmsnorm(x, w, e, o.dtype, out=o))
                 part, _, _ = gemm(xn, W)
                 cfg = rt.config
                 hd = int(attrs.get("head_dim", cfg.head_dim))
@@ -257,10 +259,28 @@ class StepPlan:
                     other = add.inputs[1] if add.inputs[0] == outs[0] else add.inputs[0]
                     resid = as_dtype(env[other], torch.float32)
                     out = buf(n, torch.float32)
-                    self.launches.append(lambda part=part, r=resid, o=out: kernels.epilogue_store(part(), o.dtype,
-                                                                                                  residual=r, out=o))
                     env[add.outputs[0]] = out
                     skip.add(graph.nodes.index(add))
+                    norm = self._normalizer(consumers.get(add.outputs[0], []), add.outputs[0])
+                    if norm is not None:
+                        # residual add and the RMSNorm that reads its result in one kernel
+                        nw_name = norm.inputs[1]
+                        nw = rt.weights.dense(nw_name, rt.dense_dtype)
+                        if norm.op == "rms_norm":
+                            xdt = input_dtype_for(norm.outputs[0]) or torch.float32
+                        else:
+                            xdt = gemm_dtype(rt.weights.matmul_weight(tuple(norm.inputs[2:5])))
+                        xn = buf(n, xdt)
+                        eps = float(norm.attrs.get("eps", 1e-6))
+                        self.launches.append(lambda part=part, r=resid, o=out, nw=nw, e=eps, xn=xn:
+                                             kernels.epilogue_residual_rmsnorm(part(), r, nw, e, o, xn))
+                        normed[(add.outputs[0], nw_name)] = xn
+                        if norm.op == "rms_norm":
+                            env[norm.outputs[0]] = xn
+                            skip.add(graph.nodes.index(norm))
+                    else:
+                        self.launches.append(lambda part=part, r=resid, o=out: kernels.epilogue_store(
+                            part(), o.dtype, residual=r, out=o))
                 else:
                     out = buf(n, torch.float32)
                     self.launches.append(lambda part=part, o=out: kernels.epilogue_store(part(), o.dtype, out=o))
@@ -293,6 +313,12 @@ class StepPlan:
             raise NotImplementedError("graph output is not a tensor value")
         self.logits = logits
         self.next_ids = torch.zeros(rows, dtype=torch.int64, device=rt.device)
+
+    @staticmethod
+    def _normalizer(users: list[Node], value: str) -> Node | None:
+        """The single RMSNorm (plain or inside a fused QKV node) that reads ``value``, if any."""
+        found = [u for u in users if (u.op == "rms_norm" or u.op in _QKV_OPS) and u.inputs[0] == value]
+        return found[0] if len(found) == 1 else None
 
     # ------------------------------------------------------------------ run ----
     def set_inputs(self, ids: np.ndarray, page_rows: np.ndarray, positions: np.ndarray) -> None:

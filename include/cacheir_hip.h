@@ -83,9 +83,10 @@ int cir_dequant(const void* weights, int tiled, int fmt, float* out, int n, int 
 /* y_partial[split][m][n] = sum over split's k-range of x[m][k] * W[n][k]
  * (the matmul of cacheir/runtime/cuda.py:920-954 / cpu.py:291-312).
  * x: fp16 [m, k] row-major (row stride ldx elements); W tiled fmt blocks.
- * Weights are dequantized to fp16 ((q-8)*d rounded once, as the reference CUDA
- * path does by casting its fp32 dequant to fp16) and multiplied on MFMA with fp32
- * accumulation.  splits must divide k/128.  Requires k % 128 == 0. */
+ * The MFMA multiplies the exact integers (q-8) (Q4_0) or q (Q8_0) in fp16 with x;
+ * each 32-value block's fp32 result is scaled by its d in fp32 (exact products:
+ * only summation order differs from the fp32 dequant-then-matmul).  fp32 accumulate.
+ * splits must divide k/128.  Requires k % 128 == 0. */
 size_t cir_qgemm_workspace_bytes(int m, int n, int splits);
 int cir_qgemm(const void* x, int ldx, const void* w_tiled, int fmt, float* y_partial,
               int m, int n, int k, int splits, void* stream);
@@ -102,6 +103,13 @@ int cir_gemm_f32(const float* x, int ldx, const float* w, float* y_partial,
  * Residual add = graph op "add" (cpu.py:256-257) fused behind o_proj / down_proj. */
 int cir_epilogue_store(const float* y_partial, int splits, const void* residual, void* out, int odt,
                        int m, int n, void* stream);
+
+/* Residual epilogue fused with the RMSNorm that consumes its result (graph ops
+ * "add" + "rms_norm", cpu.py:256-257,284-289): h = residual + sum of partials is
+ * written to h_out (fp32) and xn = (h * 1/sqrt(mean(h^2) + eps)) * norm_w (dtype
+ * xdt) is written for the next GEMM.  Rows up to 8192. */
+int cir_epilogue_residual_rmsnorm(const float* y_partial, int splits, const float* residual, float* h_out,
+                                  const void* norm_w, int wdt, float eps, void* xn, int xdt, int m, int n, void* stream);
 
 /* SwiGLU (cpu.py:266-279): y_partial columns [0, inter) are gate, [inter, 2*inter)
  * up; out[m][j] = silu(gate) * up, dtype odt. */

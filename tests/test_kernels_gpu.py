@@ -154,8 +154,9 @@ def test_qgemm_small(device, fmt, m, n, k, splits):
     ref = ops.matmul(x.astype(np.float32), wf)
     close16(got, ref)
     # products and block scales are exact in fp32: only summation order differs from an fp64 product
-    ref64 = x.astype(np.float64) @ wf.astype(np.float64).T
-    bound = 1e-5 * (np.abs(x.astype(np.float64)) @ np.abs(wf.astype(np.float64)).T) + 1e-6
+    wop = wf.astype(np.float64)
+    ref64 = x.astype(np.float64) @ wop.T
+    bound = 1e-5 * (np.abs(x.astype(np.float64)) @ np.abs(wop).T) + 1e-6
     assert np.all(np.abs(got - ref64) <= bound)
 
 

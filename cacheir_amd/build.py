@@ -31,7 +31,7 @@ def hipcc() -> str:
 
 def common_flags() -> list[str]:
     return [
-        f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-mcode-object-version=5",
+        f"--offload-arch={ARCH}", "-O3", "-std=c++20", "-fPIC", "-mcode-object-version=5",
         f"-I{ROOT / 'include'}", f"-I{SRC}",
         # Packed-FP32 VALU forms stay off in generated code (hardware notes).
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",

@@ -80,35 +80,62 @@ __global__ __launch_bounds__(kRowThreads) void rmsnorm_kernel(const TX* __restri
     o[c] = from_f32<TO>((to_f32(xr[c]) * scale) * to_f32(w[c]));
 }
 
-// Residual epilogue + RMSNorm of the result, one workgroup per row:
-// h = residual + sum_s partial_s (fp32, written to h_out) and xn = (h * rsqrt(mean(h^2)+eps)) * w.
-template <typename TW, typename TO>
+// Sum of `splits` (<= SMAX) partial planes at idx; every load is issued before the
+// adds (indices past `splits` re-read plane 0 and are dropped), in fixed order.
+template <int SMAX>
+__device__ __forceinline__ float4 split_sum4(const float* __restrict__ part, int splits, size_t plane, size_t idx) {
+  float4 v[SMAX];
+#pragma unroll
+  for (int sp = 0; sp < SMAX; ++sp) v[sp] = *reinterpret_cast<const float4*>(part + (sp < splits ? sp : 0) * plane + idx);
+  float4 t = v[0];
+#pragma unroll
+  for (int sp = 1; sp < SMAX; ++sp)
+    if (sp < splits) {
+      t.x += v[sp].x;
+      t.y += v[sp].y;
+      t.z += v[sp].z;
+      t.w += v[sp].w;
+    }
+  return t;
+}
+
+// Residual epilogue + RMSNorm of the result, one workgroup per row, 4 columns per
+// thread per step: h = residual + sum of partials (fp32, to h_out) and
+// xn = (h * rsqrt(mean(h^2) + eps)) * w.  N % 4 == 0 and N <= 8192.
+template <int SMAX, typename TW, typename TO>
 __global__ __launch_bounds__(kRowThreads) void residual_rmsnorm_kernel(
     const float* __restrict__ part, int splits, const float* __restrict__ resid, float* __restrict__ h_out,
     const TW* __restrict__ w, TO* __restrict__ xn, int M, int N, float eps) {
   __shared__ float scratch[kRowThreads / 64];
   const int r = blockIdx.x;
   const size_t plane = (size_t)M * N;
-  float v[kRowVals];
+  float4 v[2];
   float ss = 0.f;
 #pragma unroll
-  for (int i = 0; i < kRowVals; ++i) {
-    const int c = threadIdx.x + i * kRowThreads;
-    float t = 0.f;
+  for (int i = 0; i < 2; ++i) {
+    const int c = 4 * (threadIdx.x + i * kRowThreads);
+    float4 t = {0.f, 0.f, 0.f, 0.f};
     if (c < N) {
       const size_t idx = (size_t)r * N + c;
-      t = resid[idx];
-      for (int sp = 0; sp < splits; ++sp) t += part[sp * plane + idx];
-      h_out[idx] = t;
+      const float4 p = split_sum4<SMAX>(part, splits, plane, idx);
+      const float4 q = *reinterpret_cast<const float4*>(resid + idx);
+      t = make_float4(q.x + p.x, q.y + p.y, q.z + p.z, q.w + p.w);
+      *reinterpret_cast<float4*>(h_out + idx) = t;
     }
     v[i] = t;
-    ss = fmaf(t, t, ss);
+    ss += t.x * t.x + t.y * t.y + t.z * t.z + t.w * t.w;
   }
   const float scale = 1.0f / sqrtf(block_sum_1024(ss, scratch) / (float)N + eps);
 #pragma unroll
-  for (int i = 0; i < kRowVals; ++i) {
-    const int c = threadIdx.x + i * kRowThreads;
-    if (c < N) xn[(size_t)r * N + c] = from_f32<TO>((v[i] * scale) * to_f32(w[c]));
+  for (int i = 0; i < 2; ++i) {
+    const int c = 4 * (threadIdx.x + i * kRowThreads);
+    if (c < N) {
+      TO* o = xn + (size_t)r * N + c;
+      o[0] = from_f32<TO>((v[i].x * scale) * to_f32(w[c]));
+      o[1] = from_f32<TO>((v[i].y * scale) * to_f32(w[c + 1]));
+      o[2] = from_f32<TO>((v[i].z * scale) * to_f32(w[c + 2]));
+      o[3] = from_f32<TO>((v[i].w * scale) * to_f32(w[c + 3]));
+    }
   }
 }
 
@@ -131,27 +158,42 @@ __device__ __forceinline__ float split_sum(const float* __restrict__ part, int s
   return v;
 }
 
-template <typename T>
+// out = (residual +) sum of partials, 4 elements per thread (M*N % 4 == 0).
+template <int SMAX, typename T>
 __global__ void epi_store_kernel(const float* __restrict__ part, int splits, const T* __restrict__ resid,
                                  T* __restrict__ out, int M, int N) {
   const size_t n_el = (size_t)M * N;
-  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const size_t i = 4 * ((size_t)blockIdx.x * blockDim.x + threadIdx.x);
   if (i >= n_el) return;
-  float v = split_sum(part, splits, n_el, i);
-  if (resid) v = to_f32(resid[i]) + v;
-  out[i] = from_f32<T>(v);
+  float4 v = split_sum4<SMAX>(part, splits, n_el, i);
+  if (resid) {
+    v.x += to_f32(resid[i]);
+    v.y += to_f32(resid[i + 1]);
+    v.z += to_f32(resid[i + 2]);
+    v.w += to_f32(resid[i + 3]);
+  }
+  out[i] = from_f32<T>(v.x);
+  out[i + 1] = from_f32<T>(v.y);
+  out[i + 2] = from_f32<T>(v.z);
+  out[i + 3] = from_f32<T>(v.w);
 }
 
-template <typename T>
+__device__ __forceinline__ float silu_mul1(float g, float u) { return (g / (1.0f + expf(-g))) * u; }
+
+// SwiGLU over [gate | up] partial columns, 4 outputs per thread (I % 4 == 0).
+template <int SMAX, typename T>
 __global__ void epi_swiglu_kernel(const float* __restrict__ part, int splits, T* __restrict__ out, int M, int I) {
   const size_t n_el = (size_t)M * I;
-  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const size_t i = 4 * ((size_t)blockIdx.x * blockDim.x + threadIdx.x);
   if (i >= n_el) return;
   const int m = (int)(i / I), j = (int)(i % I);
   const size_t plane = (size_t)M * 2 * I;
-  const float g = split_sum(part, splits, plane, (size_t)m * 2 * I + j);
-  const float u = split_sum(part, splits, plane, (size_t)m * 2 * I + I + j);
-  out[i] = from_f32<T>((g / (1.0f + expf(-g))) * u);
+  const float4 g = split_sum4<SMAX>(part, splits, plane, (size_t)m * 2 * I + j);
+  const float4 u = split_sum4<SMAX>(part, splits, plane, (size_t)m * 2 * I + I + j);
+  out[i] = from_f32<T>(silu_mul1(g.x, u.x));
+  out[i + 1] = from_f32<T>(silu_mul1(g.y, u.y));
+  out[i + 2] = from_f32<T>(silu_mul1(g.z, u.z));
+  out[i + 3] = from_f32<T>(silu_mul1(g.w, u.w));
 }
 
 // One thread per (row, rotation pair or v element).  Columns: q [Hq*D], k [Hkv*D], v [Hkv*D].
@@ -249,6 +291,18 @@ __global__ __launch_bounds__(kRowThreads) void argmax_kernel(const float* __rest
 
 unsigned blocks_for(size_t n, unsigned bs) { return (unsigned)((n + bs - 1) / bs); }
 
+// Calls f.template operator()<SMAX>() with the smallest SMAX in {1, 2, 4, 8, 16} >= splits.
+template <typename F>
+int with_smax(int splits, F&& f) {
+  if (splits <= 1) return f.template operator()<1>();
+  if (splits <= 2) return f.template operator()<2>();
+  if (splits <= 4) return f.template operator()<4>();
+  if (splits <= 8) return f.template operator()<8>();
+  if (splits <= 16) return f.template operator()<16>();
+  set_error("epilogue: at most 16 k-splits (got %d)", splits);
+  return static_cast<int>(hipErrorInvalidValue);
+}
+
 }  // namespace
 }  // namespace cir
 
@@ -329,14 +383,17 @@ extern "C" int cir_epilogue_store(const float* y_partial, int splits, const void
                                   int n, void* stream) {
   CIR_CHECK_ARG(valid_dt(odt) && splits >= 1 && m >= 0 && n >= 0, "epilogue_store: bad arguments");
   if (m == 0 || n == 0) return 0;
+  CIR_CHECK_ARG(((size_t)m * n) % 4 == 0, "epilogue_store: m*n must be a multiple of 4");
   CIR_CHECK_ARG(y_partial && out, "epilogue_store: null pointer");
   hipStream_t s = as_stream(stream);
-  const size_t ne = (size_t)m * n;
-  if (odt == CIR_F32)
-    epi_store_kernel<float><<<blocks_for(ne, 256), 256, 0, s>>>(y_partial, splits, (const float*)residual, (float*)out, m, n);
-  else
-    epi_store_kernel<f16><<<blocks_for(ne, 256), 256, 0, s>>>(y_partial, splits, (const f16*)residual, (f16*)out, m, n);
-  return launch_status();
+  const unsigned nb = blocks_for((size_t)m * n / 4, 256);
+  return with_smax(splits, [&]<int S>() {
+    if (odt == CIR_F32)
+      epi_store_kernel<S, float><<<nb, 256, 0, s>>>(y_partial, splits, (const float*)residual, (float*)out, m, n);
+    else
+      epi_store_kernel<S, f16><<<nb, 256, 0, s>>>(y_partial, splits, (const f16*)residual, (f16*)out, m, n);
+    return launch_status();
+  });
 }
 
 extern "C" int cir_epilogue_residual_rmsnorm(const float* y_partial, int splits, const float* residual, float* h_out,
@@ -344,30 +401,37 @@ extern "C" int cir_epilogue_residual_rmsnorm(const float* y_partial, int splits,
                                              void* stream) {
   CIR_CHECK_ARG(valid_dt(wdt) && valid_dt(xdt) && splits >= 1 && m >= 0 && n >= 0, "epilogue_residual_rmsnorm: bad arguments");
   if (m == 0 || n == 0) return 0;
-  CIR_CHECK_ARG(n <= kRowVals * kRowThreads, "epilogue_residual_rmsnorm: row length %d > %d", n, kRowVals * kRowThreads);
+  CIR_CHECK_ARG(n % 4 == 0 && n <= 8 * kRowThreads, "epilogue_residual_rmsnorm: row length %d must be a multiple of 4 and <= %d",
+                n, 8 * kRowThreads);
   CIR_CHECK_ARG(y_partial && residual && h_out && norm_w && xn, "epilogue_residual_rmsnorm: null pointer");
   hipStream_t s = as_stream(stream);
-#define CIR_RR(TW, TO) \
-  residual_rmsnorm_kernel<TW, TO><<<m, kRowThreads, 0, s>>>(y_partial, splits, residual, h_out, (const TW*)norm_w, (TO*)xn, m, n, eps)
-  if (wdt == CIR_F32 && xdt == CIR_F32) CIR_RR(float, float);
-  else if (wdt == CIR_F32 && xdt == CIR_F16) CIR_RR(float, f16);
-  else if (wdt == CIR_F16 && xdt == CIR_F32) CIR_RR(f16, float);
-  else CIR_RR(f16, f16);
+  return with_smax(splits, [&]<int S>() {
+#define CIR_RR(TW, TO)                                                                                               \
+  residual_rmsnorm_kernel<S, TW, TO><<<m, kRowThreads, 0, s>>>(y_partial, splits, residual, h_out, (const TW*)norm_w, \
+                                                                (TO*)xn, m, n, eps)
+    if (wdt == CIR_F32 && xdt == CIR_F32) CIR_RR(float, float);
+    else if (wdt == CIR_F32 && xdt == CIR_F16) CIR_RR(float, f16);
+    else if (wdt == CIR_F16 && xdt == CIR_F32) CIR_RR(f16, float);
+    else CIR_RR(f16, f16);
 #undef CIR_RR
-  return launch_status();
+    return launch_status();
+  });
 }
 
 extern "C" int cir_epilogue_swiglu(const float* y_partial, int splits, void* out, int odt, int m, int inter, void* stream) {
   CIR_CHECK_ARG(valid_dt(odt) && splits >= 1 && m >= 0 && inter >= 0, "epilogue_swiglu: bad arguments");
   if (m == 0 || inter == 0) return 0;
+  CIR_CHECK_ARG(inter % 4 == 0, "epilogue_swiglu: intermediate size must be a multiple of 4");
   CIR_CHECK_ARG(y_partial && out, "epilogue_swiglu: null pointer");
   hipStream_t s = as_stream(stream);
-  const size_t ne = (size_t)m * inter;
-  if (odt == CIR_F32)
-    epi_swiglu_kernel<float><<<blocks_for(ne, 256), 256, 0, s>>>(y_partial, splits, (float*)out, m, inter);
-  else
-    epi_swiglu_kernel<f16><<<blocks_for(ne, 256), 256, 0, s>>>(y_partial, splits, (f16*)out, m, inter);
-  return launch_status();
+  const unsigned nb = blocks_for((size_t)m * inter / 4, 256);
+  return with_smax(splits, [&]<int S>() {
+    if (odt == CIR_F32)
+      epi_swiglu_kernel<S, float><<<nb, 256, 0, s>>>(y_partial, splits, (float*)out, m, inter);
+    else
+      epi_swiglu_kernel<S, f16><<<nb, 256, 0, s>>>(y_partial, splits, (f16*)out, m, inter);
+    return launch_status();
+  });
 }
 
 extern "C" int cir_epilogue_qkv_rope_append(const float* y_partial, int splits, const float* inv_freq,

@@ -41,8 +41,8 @@ def common_flags() -> list[str]:
     ]
 
 
-def _compile(src: Path, obj: Path, verbose: bool) -> None:
-    cmd = [hipcc(), *common_flags(), "-c", str(src), "-o", str(obj)]
+def _compile(src: Path, obj: Path, verbose: bool, defines: tuple[str, ...] = ()) -> None:
+    cmd = [hipcc(), *common_flags(), *(f"-D{d}" for d in defines), "-c", str(src), "-o", str(obj)]
     if verbose:
         print(" ".join(cmd), flush=True)
     proc = subprocess.run(cmd, capture_output=True, text=True)
@@ -54,23 +54,25 @@ def _compile(src: Path, obj: Path, verbose: bool) -> None:
         print(err, file=sys.stderr)
 
 
-def build(verbose: bool = False) -> Path:
-    OBJ.mkdir(parents=True, exist_ok=True)
-    LIB_DIR.mkdir(parents=True, exist_ok=True)
-    objs = [OBJ / (s.replace(".hip", ".o")) for s in SOURCES]
+def build(verbose: bool = False, defines: tuple[str, ...] = (), lib: Path = LIB, obj_dir: Path = OBJ) -> Path:
+    """Compile every source and link ``lib``.  ``defines`` (``NAME=VALUE``) and another
+    ``lib``/``obj_dir`` build a variant of the library beside the default one."""
+    obj_dir.mkdir(parents=True, exist_ok=True)
+    lib.parent.mkdir(parents=True, exist_ok=True)
+    objs = [obj_dir / (s.replace(".hip", ".o")) for s in SOURCES]
     with concurrent.futures.ThreadPoolExecutor(max_workers=len(SOURCES)) as ex:
-        futs = [ex.submit(_compile, SRC / s, o, verbose) for s, o in zip(SOURCES, objs)]
+        futs = [ex.submit(_compile, SRC / s, o, verbose, tuple(defines)) for s, o in zip(SOURCES, objs)]
         for f in futs:
             f.result()
-    tmp = LIB.with_suffix(".so.tmp")
+    tmp = lib.with_suffix(".so.tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
     if verbose:
         print(" ".join(cmd), flush=True)
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"link failed:\n{proc.stderr}")
-    os.replace(tmp, LIB)
-    return LIB
+    os.replace(tmp, lib)
+    return lib
 
 
 if __name__ == "__main__":

@@ -10,11 +10,13 @@ The stream defaults to torch's current stream (a ``hipStream_t`` on ROCm builds)
 from __future__ import annotations
 
 import ctypes
+import os
 from pathlib import Path
 
 import torch
 
-LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libcacheir_hip.so"
+# CACHEIR_HIP_LIB selects another build of the same library (e.g. one compiled with other options).
+LIB_PATH = Path(os.environ.get("CACHEIR_HIP_LIB") or Path(__file__).resolve().parent / "_lib" / "libcacheir_hip.so")
 
 CIR_F32 = 0
 CIR_F16 = 1

@@ -26,10 +26,14 @@ def _req(cond: bool, msg: str, exc=ValueError) -> None:
         raise exc(msg)
 
 
-def _cuda(t: torch.Tensor, name: str) -> None:
+def _cuda(t: torch.Tensor, name: str, rows_only: bool = False) -> None:
+    """GPU tensor check; ``rows_only`` accepts a 2-D view whose rows are contiguous (any row stride)."""
     _req(isinstance(t, torch.Tensor), f"{name} must be a torch.Tensor", TypeError)
     _req(t.is_cuda, f"{name} must be on the GPU")
-    _req(t.is_contiguous(), f"{name} must be contiguous")
+    if rows_only:
+        _req(t.dim() == 2 and t.stride(1) == 1, f"{name} rows must be contiguous")
+    else:
+        _req(t.is_contiguous(), f"{name} must be contiguous")
 
 
 # ------------------------------------------------------------------ attention --
@@ -150,16 +154,17 @@ def choose_splits(m: int, n: int, k: int) -> int:
 
 
 def qgemm_partial(x: torch.Tensor, w: QWeight, splits: int | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
-    """fp32 partials ``[splits, m, n]`` of ``x[m, k] @ W[n, k]^T`` (x fp16)."""
-    _cuda(x, "x")
+    """fp32 partials ``[splits, m, n]`` of ``x[m, k] @ W[n, k]^T`` (x fp16, rows contiguous, any row stride)."""
+    _cuda(x, "x", rows_only=True)
     _req(x.dtype == torch.float16, "qgemm activations must be float16", TypeError)
     _req(x.dim() == 2 and x.shape[1] == w.k, f"x must be [m, {w.k}]")
+    _req(x.stride(1) == 1 and x.stride(0) >= w.k, "x rows must be contiguous (row stride >= k)")
     m = x.shape[0]
     splits = choose_splits(m, w.n, w.k) if splits is None else splits
     if out is None:
         out = torch.empty((splits, m, w.n), dtype=torch.float32, device=x.device)
     _req(out.numel() >= splits * m * w.n and out.dtype == torch.float32, "partial buffer too small")
-    hip.call("cir_qgemm", x.data_ptr(), x.shape[1], w.tiled.data_ptr(), w.fmt, out.data_ptr(), m, w.n, w.k, splits,
+    hip.call("cir_qgemm", x.data_ptr(), x.stride(0), w.tiled.data_ptr(), w.fmt, out.data_ptr(), m, w.n, w.k, splits,
              hip.stream_handle())
     return out.view(-1)[: splits * m * w.n].view(splits, m, w.n)
 

@@ -76,6 +76,9 @@ def test_tiny_model_greedy_identical_fp32(tiny):
         ref = orc.run([[nxt]], mode="decode")
         np.testing.assert_allclose(logits.cpu().numpy(), ref, rtol=1e-4, atol=1e-4)
     assert ids == fx["greedy_ids"]
+    # the same ids the reference's own NumPy backend produced (make_reference_tiny.py)
+    ref_fx = json.loads((GOLDEN / "reference_tiny.json").read_text())
+    assert ref_fx["prompt"] == prompt and ids == ref_fx["greedy_ids"]
     assert rt.kv_cache.tokens == 16 + 32
     stats = rt.cache_stats()
     assert stats["kernel_counts"]

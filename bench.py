@@ -16,9 +16,15 @@ every step re-appends at the same slot and attends over exactly 2048 tokens.
 
 Printed: one JSON line with value = decode tokens/s (32 tokens per step), the
 paged-attention roofline (algorithmic bytes / live HIP-event time of the attention
-kernel, rotated over the 32 layers' KV so the 256 MB MALL cannot hold it), and a
-CPU baseline (the C/OpenMP oracle restatement timed on this host over one layer
-and the lm_head, scaled to a full step).
+kernel, rotated over the 32 layers' KV so the 256 MB MALL cannot hold it), the same
+for the largest projection (gate|up Q4_0 GEMM at m = batch, rotated over the 32
+layers' weights), and a CPU baseline (the C/OpenMP oracle restatement timed on this
+host over one layer and the lm_head, scaled to a full step).
+
+roofline.traffic is the HBM bytes per attention launch measured by rocprofv3
+FETCH_SIZE / WRITE_SIZE runs of this script, each scaled by the factor the same
+counter shows for a copy of known size (--copy-calibration adds that copy); the
+figures are read from the committed summary in profiles/ (null if it is absent).
 """
 from __future__ import annotations
 
@@ -32,6 +38,26 @@ import time
 import numpy as np
 
 HBM_PEAK_GBS = 8000.0
+TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                            "attn_f16_d128_decode_b32_ctx2048_traffic.txt")
+
+
+def measured_traffic(path: str) -> dict | None:
+    """HBM bytes per attention launch from the committed counter summary: lines
+    ``key: value`` with fetch_kib, write_kib (per dispatch) and fetch_scale, write_scale."""
+    try:
+        kv = {}
+        with open(path) as f:
+            for line in f:
+                if ":" in line and not line.lstrip().startswith("#"):
+                    k, v = line.split(":", 1)
+                    kv[k.strip()] = v.strip()
+        fetch = float(kv["fetch_kib"]) * float(kv["fetch_scale"]) * 1024
+        write = float(kv["write_kib"]) * float(kv["write_scale"]) * 1024
+        return {"bytes": round(fetch + write), "fetch": round(fetch), "write": round(write),
+                "source": os.path.relpath(path, os.path.dirname(os.path.abspath(__file__)))}
+    except (OSError, KeyError, ValueError):
+        return None
 
 
 def parse() -> argparse.Namespace:
@@ -44,6 +70,9 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--layers", type=int, default=32)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--attn-iters", type=int, default=64)
+    ap.add_argument("--gemm-iters", type=int, default=64)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="first copy 256 MiB four times (the known-size kernel for FETCH_SIZE/WRITE_SIZE scaling)")
     return ap.parse_args()
 
 
@@ -72,6 +101,14 @@ def main() -> int:
     from cacheir_amd.weights import GGML_Q4_0, SyntheticQuant
 
     dev = torch.device("cuda:0")
+    if args.copy_calibration:
+        src = torch.ones(64 * 1024 * 1024, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(4):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"calibration: copied {src.numel() * 4} bytes x4")
+        del src, dst
     cfg = llama3_8b(args.layers)
     B, ctx, P = args.batch, args.ctx, 16
     art = compile_config(cfg, quant="q4_0", modes=("decode",))
@@ -155,6 +192,26 @@ def main() -> int:
     achieved = attn_bytes / (attn_us * 1e-6) / 1e9
     log(f"attention {attn_us:.2f} us/launch, {achieved:.0f} GB/s ({achieved / HBM_PEAK_GBS:.1%} of peak)")
 
+    # ---- the same for the gate|up projection GEMM (m = batch), rotated over the layers' weights ----
+    gu = [base.weights.matmul_weight((f"layer{i}_gate_w", f"layer{i}_up_w")) for i in range(cfg.num_layers)]
+    xg = torch.randn((B, cfg.hidden_size), device=dev, dtype=torch.float16)
+    g_splits = kernels.choose_splits(B, gu[0].n, gu[0].k)
+    g_out = torch.empty((g_splits, B, gu[0].n), device=dev, dtype=torch.float32)
+    for i in range(4):
+        kernels.qgemm_partial(xg, gu[i % len(gu)], splits=g_splits, out=g_out)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for it in range(args.gemm_iters):
+        kernels.qgemm_partial(xg, gu[it % len(gu)], splits=g_splits, out=g_out)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    gemm_us = e0.elapsed_time(e1) * 1000.0 / args.gemm_iters
+    gemm_bytes = gu[0].nbytes + 2 * B * gu[0].k + 4 * g_splits * B * gu[0].n
+    gemm_gbs = gemm_bytes / (gemm_us * 1e-6) / 1e9
+    log(f"gate|up GEMM {gemm_us:.2f} us/launch (m={B}, splits {g_splits}), {gemm_gbs:.0f} GB/s")
+
+    traffic = measured_traffic(TRAFFIC_FILE)
+
     # ---- CPU baseline: C/OpenMP restatement, one layer + lm_head, scaled to the step ----
     cpu = None
     if not args.no_cpu:
@@ -163,7 +220,10 @@ def main() -> int:
         cpu = cbase.time_decode_step(batch=B, ctx=ctx, hidden=4096, ffn=14336, heads=H, kv_heads=Hkv, vocab=128256,
                                      layers=cfg.num_layers, budget_s=12.0, log=log)
 
-    weight_bytes = base.weights.nbytes()
+    # Bytes a step must move: every linear weight and norm once, the embedding rows of
+    # the batch only (the table itself is never streamed), and every layer's K/V.
+    embed = base.weights.dense("tok_embeddings", torch.float16)
+    weight_bytes = base.weights.nbytes() - embed.numel() * embed.element_size() + B * cfg.hidden_size * 2
     line = {
         "metric": "decode tokens/s, batch 32, Llama-3-8B-shape Q4_0; paged-attn HBM GB/s",
         "value": round(toks, 2),
@@ -179,10 +239,16 @@ def main() -> int:
         "data": "synthetic: random-init Q4_0 weights, N(0,1) fp16 KV context",
         "config": {"workload": "BASELINE config 4: Llama-3-8B-shape Q4_0 full decode step", "batch": B,
                    "context": ctx, "layers": cfg.num_layers, "page_size": P, "parallelism": "single GPU"},
-        "roofline": {"bound": "hbm", "kernel": "paged decode attention (attn_chunk_f16_d128<4>)",
+        "roofline": {"bound": "hbm", "kernel": "paged decode attention (attn_f16_d128<4>)",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": traffic["bytes"] if traffic else None,
+                     "traffic_detail": traffic,
                      "bytes_per_launch": attn_bytes, "us_per_launch": round(attn_us, 3)},
+        "roofline_gemm": {"bound": "hbm", "kernel": f"Q4_0 gate|up GEMM m={B} (qgemm_kernel)",
+                          "achieved": round(gemm_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                          "frac": round(gemm_gbs / HBM_PEAK_GBS, 4), "bytes_per_launch": gemm_bytes,
+                          "us_per_launch": round(gemm_us, 3), "splits": g_splits},
         "step_bytes": {"weights": weight_bytes, "kv": kv_bytes * cfg.num_layers,
                        "hbm_floor_ms": round((weight_bytes + kv_bytes * cfg.num_layers) / HBM_PEAK_GBS / 1e6, 4)},
         "cpu_baseline": cpu,

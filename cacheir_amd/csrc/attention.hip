@@ -35,14 +35,8 @@
 namespace cir {
 namespace {
 
-#ifndef CIR_ATTN_WAVES
-#define CIR_ATTN_WAVES 8
-#endif
-#ifndef CIR_ATTN_KFIRST
-#define CIR_ATTN_KFIRST 1
-#endif
 constexpr int kBlock = 64;   // tokens per wavefront step (4 MFMA tiles of 16)
-constexpr int kWaves = CIR_ATTN_WAVES;    // wavefronts per workgroup (fp16 path)
+constexpr int kWaves = 8;    // wavefronts per workgroup (fp16 path; 16 measured slower)
 constexpr int kChunk = 128;  // tokens per partial in the generic path
 constexpr int kMinSplitTokens = 256;
 constexpr float kLog2e = 1.4426950408889634f;
@@ -104,9 +98,9 @@ __global__ __launch_bounds__(64 * kWaves) void attn_f16_d128(
 
   for (int blk = b0 + wave; blk < b1; blk += kWaves) {
     const int tb = blk * kBlock;
-    // Issue every K and V load of the block before using any of them.
+    // Issue every K load, then every V load, of the block before using any of them
+    // (K first: the scores need only K, so they start while V is still arriving).
     f16x8 kb[4][4], vb[4][4];
-#if CIR_ATTN_KFIRST
     size_t base[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -127,21 +121,6 @@ __global__ __launch_bounds__(64 * kWaves) void attn_f16_d128(
 #pragma unroll
       for (int u = 0; u < 4; ++u) vb[j][u] = *reinterpret_cast<const f16x8*>(vrow + (size_t)(4 * u + lg) * D);
     }
-#else
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int tj = tb + 16 * j;
-      const int tv = tj < L ? tj : tb;  // tiles past the end re-read tile 0 (masked below)
-      const int page = ptrow[tv / P];
-      const size_t base = (((size_t)page * Hkv + kvh) * P + (tv % P)) * D;
-      const f16* krow = kp + base + (size_t)li * D + 8 * lg;
-      const f16* vrow = vp + base + 8 * li;
-#pragma unroll
-      for (int s = 0; s < 4; ++s) kb[j][s] = *reinterpret_cast<const f16x8*>(krow + 32 * s);
-#pragma unroll
-      for (int u = 0; u < 4; ++u) vb[j][u] = *reinterpret_cast<const f16x8*>(vrow + (size_t)(4 * u + lg) * D);
-    }
-#endif
     // Keep all 32 loads ahead of their first use (the scheduler would otherwise
     // interleave them with the MFMAs and leave one 1 KiB load in flight).
     __builtin_amdgcn_sched_barrier(0);

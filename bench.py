@@ -245,7 +245,7 @@ def main() -> int:
                      "traffic": traffic["bytes"] if traffic else None,
                      "traffic_detail": traffic,
                      "bytes_per_launch": attn_bytes, "us_per_launch": round(attn_us, 3)},
-        "roofline_gemm": {"bound": "hbm", "kernel": f"Q4_0 gate|up GEMM m={B} (qgemm_kernel)",
+        "roofline_gemm": {"bound": "hbm", "kernel": f"Q4_0 gate|up GEMM m={B} (qgemm_xs_kernel)",
                           "achieved": round(gemm_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                           "frac": round(gemm_gbs / HBM_PEAK_GBS, 4), "bytes_per_launch": gemm_bytes,
                           "us_per_launch": round(gemm_us, 3), "splits": g_splits},

@@ -28,11 +28,13 @@
 //   reference CUDA path does at cuda.py:935, misses the 2e-3 + 1e-2|y| bound at
 //   k = 14336.)
 //
-// GEMM: workgroup = 4 wavefronts on the same NT*16 output rows; the wavefronts
-// interleave over the quads of the workgroup's k-range and their fp32 accumulators
-// are summed through LDS.  grid.y splits k further (partials summed by the
-// epilogue kernels); grid.z walks 16*MT-row blocks of x.
+// GEMM (qgemm_xs_kernel): workgroup = 4 wavefronts on 4*NT*16 output rows; they walk
+// the quads of the workgroup's k-range in lock step and share each quad of
+// activations through LDS.  grid.y splits k (fp32 partials, summed by the epilogue
+// kernels); grid.z walks 16*MT-row blocks of x.
 #include "common.hpp"
+
+#include <utility>
 
 namespace cir {
 namespace {
@@ -182,7 +184,8 @@ __global__ void dequant_tiled_kernel(const uint8_t* __restrict__ q, const uint16
 }
 
 // ------------------------------------------------------------------ GEMM -----
-// One quad (128 columns) of operands for one wavefront: NT weight tiles and MT x tiles.
+// One quad (128 columns) of operands for one wavefront: NT weight tiles (codes and
+// scales) and the MT activation tiles as MFMA A operands.
 template <int FMT, int NT, int MT>
 struct Stage {
   static constexpr int LB = (FMT == CIR_Q4_0) ? 1 : 2;  // 16-byte loads per lane per weight tile
@@ -190,25 +193,6 @@ struct Stage {
   uint2 d[NT];
   f16x8 x[MT][4];
 };
-
-// wbase[b] / dbase[b] point at tile (nt0 + b, quad 0) for this lane; quads are
-// consecutive tiles, so quad Q is Q tile-strides further.
-template <int FMT, int NT, int MT>
-__device__ __forceinline__ void load_stage(Stage<FMT, NT, MT>& st, const uint4* const (&wbase)[NT],
-                                           const uint2* const (&dbase)[NT], const f16* const (&xrow)[MT], int Q) {
-  constexpr int LB = Stage<FMT, NT, MT>::LB;
-#pragma unroll
-  for (int b = 0; b < NT; ++b) {
-    const uint4* src = wbase[b] + (size_t)Q * (64 * LB);
-#pragma unroll
-    for (int c = 0; c < LB; ++c) st.w[b][c] = src[c];
-    st.d[b] = dbase[b][(size_t)Q * 16];
-  }
-#pragma unroll
-  for (int a = 0; a < MT; ++a)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) st.x[a][j] = *reinterpret_cast<const f16x8*>(xrow[a] + 128 * Q + 32 * j);
-}
 
 // Exact integer weights ((q - 8) for Q4_0, q for Q8_0) feed one MFMA per 32-value
 // block; the block's fp32 result is scaled by d in fp32 and accumulated.  All MFMAs
@@ -244,86 +228,6 @@ __device__ __forceinline__ void compute_stage(const Stage<FMT, NT, MT>& st, f32x
   }
 }
 
-// FMT: CIR_Q4_0 or CIR_Q8_0.  NT: 16-row n-tiles per wavefront.  MT: 16-row m-tiles.
-// The four wavefronts of a workgroup take every fourth quad of the split; each
-// wavefront prefetches its next quad while it computes the current one.
-template <int FMT, int NT, int MT>
-__global__ __launch_bounds__(256) void qgemm_kernel(const f16* __restrict__ x, int ldx, const uint8_t* __restrict__ wq,
-                                                    const uint16_t* __restrict__ wd, float* __restrict__ part, int M,
-                                                    int N, int K, int quads_per_split) {
-  __shared__ f32x4 red[3][MT * NT][64];
-  constexpr int LB = Stage<FMT, NT, MT>::LB;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: keeps the quad loop scalar
-  const int lane = threadIdx.x & 63;
-  const int li = lane & 15, lg = lane >> 4;
-  const int KQ = K / 128;
-  const int NTILES = (N + 15) / 16;
-  const int nt0 = blockIdx.x * NT;
-  const int split = blockIdx.y;
-  const int m0 = blockIdx.z * 16 * MT;
-  const int qe = split * quads_per_split + quads_per_split;
-
-  f32x4 acc[MT][NT];
-#pragma unroll
-  for (int a = 0; a < MT; ++a)
-#pragma unroll
-    for (int b = 0; b < NT; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  // Rows past M read row M-1 (valid memory); their results are never stored.
-  const f16* xrow[MT];
-#pragma unroll
-  for (int a = 0; a < MT; ++a) xrow[a] = x + (size_t)min(m0 + 16 * a + li, M - 1) * ldx + 8 * lg;
-  const uint4* wbase[NT];
-  const uint2* dbase[NT];
-#pragma unroll
-  for (int b = 0; b < NT; ++b) {
-    const size_t tile0 = (size_t)min(nt0 + b, NTILES - 1) * KQ;  // tiles past N re-read the last tile
-    wbase[b] = reinterpret_cast<const uint4*>(wq) + (tile0 * 64 + lane) * LB;
-    dbase[b] = reinterpret_cast<const uint2*>(wd) + tile0 * 16 + li;
-  }
-
-  Stage<FMT, NT, MT> s0, s1;
-  int Q = split * quads_per_split + wave;
-  if (Q < qe) load_stage(s0, wbase, dbase, xrow, Q);
-  while (Q < qe) {
-    if (Q + 4 < qe) load_stage(s1, wbase, dbase, xrow, Q + 4);
-    compute_stage(s0, acc);
-    Q += 4;
-    if (Q >= qe) break;
-    if (Q + 4 < qe) load_stage(s0, wbase, dbase, xrow, Q + 4);
-    compute_stage(s1, acc);
-    Q += 4;
-  }
-
-  // Sum the four wavefronts' accumulators through LDS; wavefront 0 writes.
-  if (wave > 0) {
-#pragma unroll
-    for (int a = 0; a < MT; ++a)
-#pragma unroll
-      for (int b = 0; b < NT; ++b) red[wave - 1][a * NT + b][lane] = acc[a][b];
-  }
-  __syncthreads();
-  if (wave == 0) {
-#pragma unroll
-    for (int a = 0; a < MT; ++a)
-#pragma unroll
-      for (int b = 0; b < NT; ++b) {
-        f32x4 v = acc[a][b];
-        v += red[0][a * NT + b][lane];
-        v += red[1][a * NT + b][lane];
-        v += red[2][a * NT + b][lane];
-        const int n = (nt0 + b) * 16 + li;
-        if (nt0 + b < NTILES && n < N) {
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int m = m0 + 16 * a + 4 * lg + r;
-            if (m < M) part[((size_t)split * M + m) * N + n] = v[r];
-          }
-        }
-      }
-  }
-}
-
 // Dense fp32: one wavefront per output row n, lanes over k; all m rows.
 __global__ __launch_bounds__(256) void gemm_f32_kernel(const float* __restrict__ x, int ldx, const float* __restrict__ w,
                                                        float* __restrict__ part, int M, int N, int K, int kc) {
@@ -342,28 +246,181 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(const float* __restrict__
   }
 }
 
-template <int FMT, int NT, int MT>
-void launch_qgemm(const f16* x, int ldx, const uint8_t* wq, const uint16_t* wd, float* part, int M, int N, int K,
-                  int splits, hipStream_t s) {
+// ---------------------------------------------------------- x-shared GEMM ---
+// The four wavefronts of a workgroup own different output tiles (NT each) and walk
+// the same k-quads in lock step, so each quad of activations is read from L2 once
+// per workgroup (cooperatively, 16 B per thread per 16-row tile) and shared through
+// LDS, instead of once per wavefront.  Weights stream through a ring of DW stages
+// per wavefront; each stage's activation loads are issued before its weight loads,
+// so waiting for the activations of quad i+1 never waits for weights issued later.
+// One workgroup barrier per quad: it publishes the activation slot written for
+// quad i+1 and releases the slot read for quad i.
+constexpr int kXsRowBytes = 272;  // 128 fp16 + 16 B pad: the 16 rows of a fragment read hit different banks
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // plain vector: no struct memcpy, stays in VGPRs
+
+template <int MT>
+struct XsChunk {  // this thread's share of one quad of activations
+  u32x4 v[MT];
+};
+
+template <int FMT, int NT, int MT, int DW>
+__global__ __launch_bounds__(256) void qgemm_xs_kernel(const f16* __restrict__ x, int ldx,
+                                                       const uint8_t* __restrict__ wq, const uint16_t* __restrict__ wd,
+                                                       float* __restrict__ part, int M, int N, int K,
+                                                       int quads_per_split) {
+  constexpr int LB = Stage<FMT, NT, MT>::LB;
+  __shared__ __align__(16) uint8_t xs[2][16 * MT * kXsRowBytes];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int li = lane & 15, lg = lane >> 4;
+  const int KQ = K / 128;
   const int NTILES = (N + 15) / 16;
-  dim3 grid((NTILES + NT - 1) / NT, splits, (M + 16 * MT - 1) / (16 * MT));
-  qgemm_kernel<FMT, NT, MT><<<grid, 256, 0, s>>>(x, ldx, wq, wd, part, M, N, K, (K / 128) / splits);
+  const int nt0 = (blockIdx.x * 4 + wave) * NT;  // this wavefront's first tile
+  const int split = blockIdx.y;
+  const int m0 = blockIdx.z * 16 * MT;
+  const int q0 = split * quads_per_split;
+  const int nq = quads_per_split;
+
+  // Cooperative activation chunk of this thread: row r = c / 16, 16-byte column c % 16.
+  const f16* xsrc[MT];
+  int xdst[MT];
+#pragma unroll
+  for (int u = 0; u < MT; ++u) {
+    const int c = threadIdx.x + 256 * u;
+    const int r = c >> 4, col = c & 15;
+    xsrc[u] = x + (size_t)min(m0 + r, M - 1) * ldx + 8 * col;  // rows past M re-read row M-1 (never stored)
+    xdst[u] = r * kXsRowBytes + 16 * col;
+  }
+  const uint4* wbase[NT];
+  const uint2* dbase[NT];
+#pragma unroll
+  for (int b = 0; b < NT; ++b) {
+    const size_t tile0 = (size_t)min(nt0 + b, NTILES - 1) * KQ;
+    wbase[b] = reinterpret_cast<const uint4*>(wq) + (tile0 * 64 + lane) * LB;
+    dbase[b] = reinterpret_cast<const uint2*>(wd) + tile0 * 16 + li;
+  }
+
+  struct WS {
+    uint4 w[NT][LB];
+    uint2 d[NT];
+  };
+  WS ws[DW];
+  XsChunk<MT> xc[DW];
+  // (always_inline: a ring slot index must fold to a constant, or the rings go to scratch)
+  auto issue = [&](int slot_w, int idx) __attribute__((always_inline)) {  // stage idx (clamped to the last quad)
+    const int Q = q0 + min(idx, nq - 1);
+#pragma unroll
+    for (int u = 0; u < MT; ++u) xc[slot_w].v[u] = *reinterpret_cast<const u32x4*>(xsrc[u] + 128 * Q);
+#pragma unroll
+    for (int b = 0; b < NT; ++b) {
+      const uint4* src = wbase[b] + (size_t)Q * (64 * LB);
+#pragma unroll
+      for (int c = 0; c < LB; ++c) ws[slot_w].w[b][c] = src[c];
+      ws[slot_w].d[b] = dbase[b][(size_t)Q * 16];
+    }
+  };
+  auto put_x = [&](int slot_x, const XsChunk<MT>& ch) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < MT; ++u) *reinterpret_cast<u32x4*>(&xs[slot_x][xdst[u]]) = ch.v[u];
+  };
+  auto barrier = [] { __syncthreads(); };
+
+  f32x4 acc[MT][NT];
+#pragma unroll
+  for (int a = 0; a < MT; ++a)
+#pragma unroll
+    for (int b = 0; b < NT; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  auto compute = [&](const WS& st, int slot_x) __attribute__((always_inline)) {
+    Stage<FMT, NT, MT> sg;  // reuse compute_stage: fragments from LDS, weights from the ring
+#pragma unroll
+    for (int a = 0; a < MT; ++a)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        sg.x[a][j] = *reinterpret_cast<const f16x8*>(&xs[slot_x][(16 * a + li) * kXsRowBytes + 64 * j + 16 * lg]);
+#pragma unroll
+    for (int b = 0; b < NT; ++b) {
+#pragma unroll
+      for (int c = 0; c < LB; ++c) sg.w[b][c] = st.w[b][c];
+      sg.d[b] = st.d[b];
+    }
+    compute_stage(sg, acc);
+  };
+
+  // Ring slots are template arguments (std::integer_sequence), so every ring access
+  // has a compile-time index and the rings stay in registers.
+  auto each = [&](auto&& f) __attribute__((always_inline)) {
+    [&]<int... S>(std::integer_sequence<int, S...>) { (f.template operator()<S>(), ...); }(
+        std::make_integer_sequence<int, DW>{});
+  };
+  // Prologue: stages 0 .. DW-1 in flight, activations of quad 0 in LDS slot 0.
+  each([&]<int S>() { issue(S, S); });
+  put_x(0, xc[0]);
+  barrier();
+  // Steady state: at index i + S publish x(i+S+1), compute quad i+S, then refill
+  // ring slot S with stage i+S+DW.  The LDS slot of quad idx is idx & 1.
+  int i = 0;
+  for (; i + DW <= nq; i += DW) {
+    each([&]<int S>() {
+      put_x((i + S + 1) & 1, xc[(S + 1) % DW]);
+      compute(ws[S], (i + S) & 1);
+      issue(S, i + S + DW);
+      barrier();
+    });
+  }
+  each([&]<int S>() {
+    if (S < DW - 1 && i + S < nq) {
+      put_x((i + S + 1) & 1, xc[(S + 1) % DW]);
+      compute(ws[S], (i + S) & 1);
+      barrier();
+    }
+  });
+
+#pragma unroll
+  for (int a = 0; a < MT; ++a)
+#pragma unroll
+    for (int b = 0; b < NT; ++b) {
+      const int n = (nt0 + b) * 16 + li;
+      if (nt0 + b < NTILES && n < N) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int m = m0 + 16 * a + 4 * lg + r;
+          if (m < M) part[((size_t)split * M + m) * N + n] = acc[a][b][r];
+        }
+      }
+    }
 }
 
-// NT = 4 (64 rows per workgroup, best x reuse) unless that leaves fewer than ~256
-// workgroups, then NT = 2.
+template <int FMT, int NT, int MT, int DW>
+void launch_qgemm_xs(const f16* x, int ldx, const uint8_t* wq, const uint16_t* wd, float* part, int M, int N, int K,
+                     int splits, hipStream_t s) {
+  const int NTILES = (N + 15) / 16;
+  dim3 grid((NTILES + 4 * NT - 1) / (4 * NT), splits, (M + 16 * MT - 1) / (16 * MT));
+  qgemm_xs_kernel<FMT, NT, MT, DW><<<grid, 256, 0, s>>>(x, ldx, wq, wd, part, M, N, K, (K / 128) / splits);
+}
+
+// Workgroup rows: 4 wavefronts x NT tiles x 16.  m <= 16 takes NT = 1 (64 rows per
+// workgroup, MT = 1); larger m takes NT = 2, MT = 2 (128 rows x 32 activation rows):
+// each activation quad then feeds 8 weight tiles.  Measured on MI355X at the
+// Llama-3-8B shapes (m = 1, 8, 32) against NT = 4 and ring depths 2..6.
+constexpr int xs_rows_per_group(int m) { return m <= 16 ? 64 : 128; }
+
+// k-split: the smallest power of two that gives >= 256 workgroups, keeping at least
+// 4 quads per split (split-k partials cost 4*m*n bytes each, so no more than needed).
+int default_splits(int m, int n, int k) {
+  const int kq = k / 128;
+  const long groups = (long)((n + xs_rows_per_group(m) - 1) / xs_rows_per_group(m)) * ((m + 31) / 32);
+  int s = 1;
+  while (groups * s < 256 && kq % (2 * s) == 0 && kq / (2 * s) >= 4) s *= 2;
+  return s;
+}
+
 template <int FMT>
 void dispatch_qgemm(const f16* x, int ldx, const uint8_t* wq, const uint16_t* wd, float* part, int M, int N, int K,
                     int splits, hipStream_t s) {
-  const long groups4 = (long)((N + 63) / 64) * splits * ((M + 31) / 32);
-  const bool wide = groups4 >= 256;
-  if (M <= 16) {
-    if (wide) launch_qgemm<FMT, 4, 1>(x, ldx, wq, wd, part, M, N, K, splits, s);
-    else launch_qgemm<FMT, 2, 1>(x, ldx, wq, wd, part, M, N, K, splits, s);
-  } else {
-    if (wide) launch_qgemm<FMT, 4, 2>(x, ldx, wq, wd, part, M, N, K, splits, s);
-    else launch_qgemm<FMT, 2, 2>(x, ldx, wq, wd, part, M, N, K, splits, s);
-  }
+  if (M <= 16) launch_qgemm_xs<FMT, 1, 1, 4>(x, ldx, wq, wd, part, M, N, K, splits, s);
+  else launch_qgemm_xs<FMT, 2, 2, 4>(x, ldx, wq, wd, part, M, N, K, splits, s);
 }
 
 }  // namespace
@@ -410,6 +467,11 @@ extern "C" int cir_dequant(const void* weights, int tiled, int fmt, float* out, 
     dequant_tiled_kernel<<<(unsigned)((threads + 255) / 256), 256, 0, s>>>(q, d, out, fmt, n, k);
   }
   return launch_status();
+}
+
+extern "C" int cir_qgemm_splits(int m, int n, int k) {
+  if (m <= 0 || n <= 0 || k <= 0 || k % 128) return 0;
+  return cir::default_splits(m, n, k);
 }
 
 extern "C" size_t cir_qgemm_workspace_bytes(int m, int n, int splits) {

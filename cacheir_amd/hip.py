@@ -37,6 +37,7 @@ _SIGNATURES = {
     "cir_qweight_tiled_bytes": (_c_size, [_c_int, _c_int, _c_int]),
     "cir_qweight_repack": (_c_int, [_vp, _vp, _c_int, _c_int, _c_int, _vp]),
     "cir_dequant": (_c_int, [_vp, _c_int, _c_int, _vp, _c_int, _c_int, _vp]),
+    "cir_qgemm_splits": (_c_int, [_c_int, _c_int, _c_int]),
     "cir_qgemm_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int]),
     "cir_qgemm": (_c_int, [_vp, _c_int, _vp, _c_int, _vp, _c_int, _c_int, _c_int, _c_int, _vp]),
     "cir_gemm_f32": (_c_int, [_vp, _c_int, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp]),

@@ -143,14 +143,10 @@ def dequant_tiled(w: QWeight) -> torch.Tensor:
 
 
 def choose_splits(m: int, n: int, k: int) -> int:
-    """k-split for the tiled GEMM: enough workgroups to cover the GPU (≈ 2 per CU)."""
-    quads = k // 128
-    n_groups = (n + 63) // 64
-    m_groups = (m + 31) // 32
-    splits = 1
-    while n_groups * m_groups * splits < 512 and quads % (splits * 2) == 0 and quads // (splits * 2) >= 4:
-        splits *= 2
-    return splits
+    """k-split the library tunes ``cir_qgemm`` for at this shape (``cir_qgemm_splits``)."""
+    s = hip.load().cir_qgemm_splits(m, n, k)
+    _req(s > 0, f"no k-split for shape m={m} n={n} k={k} (k must be a positive multiple of 128)")
+    return s
 
 
 def qgemm_partial(x: torch.Tensor, w: QWeight, splits: int | None = None, out: torch.Tensor | None = None) -> torch.Tensor:

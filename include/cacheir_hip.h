@@ -80,6 +80,12 @@ int cir_qweight_repack(const void* gguf_blocks, void* tiled, int fmt, int n, int
  * tiled copy (tiled = 1).  Replaces gguf.py:273-310 for device-resident weights. */
 int cir_dequant(const void* weights, int tiled, int fmt, float* out, int n, int k, void* stream);
 
+/* The k-split cir_qgemm is tuned for at this shape (a power of two dividing k/128):
+ * enough workgroups to fill the GPU, no more partials than that needs.  0 for an
+ * invalid shape.  (The reference has no k-split; this replaces its GEMM plan choice,
+ * cacheir/runtime/cuda.py:956-974 _select_gemm_plan.) */
+int cir_qgemm_splits(int m, int n, int k);
+size_t cir_qgemm_workspace_bytes(int m, int n, int splits);
 /* y_partial[split][m][n] = sum over split's k-range of x[m][k] * W[n][k]
  * (the matmul of cacheir/runtime/cuda.py:920-954 / cpu.py:291-312).
  * x: fp16 [m, k] row-major (row stride ldx elements); W tiled fmt blocks.
@@ -87,7 +93,6 @@ int cir_dequant(const void* weights, int tiled, int fmt, float* out, int n, int 
  * each 32-value block's fp32 result is scaled by its d in fp32 (exact products:
  * only summation order differs from the fp32 dequant-then-matmul).  fp32 accumulate.
  * splits must divide k/128.  Requires k % 128 == 0. */
-size_t cir_qgemm_workspace_bytes(int m, int n, int splits);
 int cir_qgemm(const void* x, int ldx, const void* w_tiled, int fmt, float* y_partial,
               int m, int n, int k, int splits, void* stream);
 

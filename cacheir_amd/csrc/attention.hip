@@ -8,9 +8,9 @@
 // few splits whose (max, sum, O) partials a small merge kernel combines.
 //
 // fp16 pools, head_dim 128 (Llama-3 / Qwen2 shapes), 8 wavefronts per workgroup:
-//   * the split's context is cut into 64-token blocks dealt round-robin to the
+//   * the split's context is cut into 32-token blocks dealt round-robin to the
 //     wavefronts; a wavefront issues every K and V load of its block up front
-//     (16 KiB of K and 16 KiB of V in flight, no branches: tiles past the end are
+//     (8 KiB of K and 8 KiB of V in flight, no branches: tiles past the end are
 //     clamped to a valid page and masked);
 //   * S = Q K^T on MFMA 16x16x32 f16: A = the group's query heads padded to 16
 //     rows, B = a 16-token tile of K read straight from its page (token rows of
@@ -35,8 +35,13 @@
 namespace cir {
 namespace {
 
-constexpr int kBlock = 64;   // tokens per wavefront step (4 MFMA tiles of 16)
-constexpr int kWaves = 8;    // wavefronts per workgroup (fp16 path; 16 measured slower)
+// 8 wavefronts of 32-token steps measured best on MI355X at config 4 (batch 32,
+// 2048 tokens): 53.7 us = 5.0 TB/s against 61 us for 64-token steps, 56 us for 16
+// wavefronts of 16 tokens and 55 us for a double-buffered 16-token pipeline.  A pure
+// streaming read peaks at ~6.2 TB/s on this part.
+constexpr int kTiles = 2;             // 16-token MFMA tiles per wavefront step
+constexpr int kBlock = 16 * kTiles;   // tokens per wavefront step
+constexpr int kWaves = 8;             // wavefronts per workgroup (fp16 path)
 constexpr int kChunk = 128;  // tokens per partial in the generic path
 constexpr int kMinSplitTokens = 256;
 constexpr float kLog2e = 1.4426950408889634f;
@@ -50,16 +55,36 @@ __device__ __forceinline__ int visible_len(const int32_t* lens, int row, int q_l
 
 // ----------------------------------------------------------------------------
 // fp16 pools, head_dim 128.  G = query heads per KV head (1..8).
+// Fused decode input (optional): the QKV projection's fp32 split-k partials
+// [splits][batch][(Hq + 2 Hkv) D] instead of a finished q.  The workgroup then sums
+// its heads' partials, applies RoPE to q and k, appends the new k and v to their page
+// and keeps q in LDS -- the work of the QKV epilogue kernel, in the same order and
+// precision, for one (row, KV head) at a time.
+struct QkvIn {
+  const float* part;        // null: q is read from `q`
+  int splits;
+  const float* inv_freq;    // [D/2]
+  const int32_t* positions; // [batch]: position of the new token
+};
+
+// Sum over the splits in split order (bitwise as the epilogue kernels sum).
+__device__ __forceinline__ float sum_splits(const float* __restrict__ p, int splits, size_t plane, size_t idx) {
+  float v = p[idx];
+  for (int s = 1; s < splits; ++s) v += p[(size_t)s * plane + idx];
+  return v;
+}
+
 template <int G>
 __global__ __launch_bounds__(64 * kWaves) void attn_f16_d128(
-    const f16* __restrict__ q, const f16* __restrict__ kp, const f16* __restrict__ vp,
+    const f16* __restrict__ q, f16* __restrict__ kp, f16* __restrict__ vp,
     const int32_t* __restrict__ pt, const int32_t* __restrict__ lens, f16* __restrict__ out,
     float* __restrict__ part_o, float* __restrict__ part_ml, int q_len, int Hq, int Hkv, int P, int max_pages,
-    int S, float scale_log2) {
+    int S, float scale_log2, QkvIn qkv) {
   constexpr int D = 128;
   __shared__ float sm_m[kWaves][16];
   __shared__ float sm_l[kWaves][16];
   __shared__ float sm_o[kWaves][G][D];
+  __shared__ __align__(16) f16 sm_q[G][D];
 
   const int split = blockIdx.x, kvh = blockIdx.y, row = blockIdx.z;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -72,11 +97,52 @@ __global__ __launch_bounds__(64 * kWaves) void attn_f16_d128(
   const int b = row / q_len;
   const int32_t* ptrow = pt + (size_t)b * max_pages;
 
+  if (qkv.part) {  // fused decode input (q_len == 1): q, k, v of this row and KV head
+    const int pos = qkv.positions[b];
+    const int N = (Hq + 2 * Hkv) * D;
+    const size_t plane = (size_t)gridDim.z * N;
+    const float* base = qkv.part + (size_t)row * N;
+    const int page_idx = pos / P;
+    const int slot = (page_idx < max_pages) ? ptrow[page_idx] : -1;
+    const int off = pos - page_idx * P;
+    // The split whose blocks hold the new token appends it (and alone reads it back).
+    const bool writer = split == min(S - 1, (pos / kBlock) / max(per, 1));
+    constexpr int kHalf = D / 2;
+    for (int it = threadIdx.x; it < (G + 1) * kHalf + D; it += 64 * kWaves) {
+      if (it < (G + 1) * kHalf) {  // RoPE pair i of q head hh (hh < G) or of k (hh == G)
+        const int hh = it / kHalf, i = it - hh * kHalf;
+        const size_t col0 = (hh < G ? ((size_t)kvh * G + hh) * D : (size_t)Hq * D + (size_t)kvh * D) + 2 * i;
+        const float x0 = sum_splits(base, qkv.splits, plane, col0);
+        const float x1 = sum_splits(base, qkv.splits, plane, col0 + 1);
+        float sn, cs;
+        sincosf((float)pos * qkv.inv_freq[i], &sn, &cs);
+        const float y0 = x0 * cs - x1 * sn;
+        const float y1 = x0 * sn + x1 * cs;
+        if (hh < G) {
+          sm_q[hh][2 * i] = static_cast<f16>(y0);
+          sm_q[hh][2 * i + 1] = static_cast<f16>(y1);
+        } else if (writer && slot >= 0) {
+          f16* o = kp + (((size_t)slot * Hkv + kvh) * P + off) * D + 2 * i;
+          o[0] = static_cast<f16>(y0);
+          o[1] = static_cast<f16>(y1);
+        }
+      } else {
+        const int d = it - (G + 1) * kHalf;
+        const float v = sum_splits(base, qkv.splits, plane, (size_t)(Hq + Hkv) * D + (size_t)kvh * D + d);
+        if (writer && slot >= 0) vp[(((size_t)slot * Hkv + kvh) * P + off) * D + d] = static_cast<f16>(v);
+      }
+    }
+    // Publishes q in LDS and the appended k/v (global stores before a workgroup barrier
+    // are visible to the workgroup; no wavefront has read that page line yet).
+    __syncthreads();
+  }
+
   // Q as the MFMA A operand: row li = head kvh*G + li (zero rows past G); element e
   // of step s is head dim 32*s + 8*lg + e, the same mapping the K loads use.
   f16x8 qa[4];
   {
-    const f16* qrow = q + ((size_t)row * Hq + (size_t)kvh * G + (li < G ? li : 0)) * D + 8 * lg;
+    const f16* qrow = qkv.part ? &sm_q[li < G ? li : 0][8 * lg]
+                               : q + ((size_t)row * Hq + (size_t)kvh * G + (li < G ? li : 0)) * D + 8 * lg;
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       const f16x8 v = *reinterpret_cast<const f16x8*>(qrow + 32 * s);
@@ -96,41 +162,45 @@ __global__ __launch_bounds__(64 * kWaves) void attn_f16_d128(
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[h][e] = 0.f;
 
-  for (int blk = b0 + wave; blk < b1; blk += kWaves) {
+  // One block of K/V operands (kTiles 16-token tiles) for one wavefront.
+  struct Blk {
+    f16x8 k[kTiles][4], v[kTiles][4];
+  };
+  // Issue every K load, then every V load, of block `blk` (K first: the scores need
+  // only K, so they start while V is still arriving).  Tiles past the end re-read
+  // the block's first tile (masked in the scores).
+  auto load_block = [&](Blk& o, int blk) __attribute__((always_inline)) {
     const int tb = blk * kBlock;
-    // Issue every K load, then every V load, of the block before using any of them
-    // (K first: the scores need only K, so they start while V is still arriving).
-    f16x8 kb[4][4], vb[4][4];
-    size_t base[4];
+    size_t base[kTiles];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < kTiles; ++j) {
       const int tj = tb + 16 * j;
-      const int tv = tj < L ? tj : tb;  // tiles past the end re-read tile 0 (masked below)
+      const int tv = tj < L ? tj : tb;
       const int page = ptrow[tv / P];
       base[j] = (((size_t)page * Hkv + kvh) * P + (tv % P)) * D;
     }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < kTiles; ++j) {
       const f16* krow = kp + base[j] + (size_t)li * D + 8 * lg;
 #pragma unroll
-      for (int s = 0; s < 4; ++s) kb[j][s] = *reinterpret_cast<const f16x8*>(krow + 32 * s);
+      for (int s = 0; s < 4; ++s) o.k[j][s] = *reinterpret_cast<const f16x8*>(krow + 32 * s);
     }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < kTiles; ++j) {
       const f16* vrow = vp + base[j] + 8 * li;
 #pragma unroll
-      for (int u = 0; u < 4; ++u) vb[j][u] = *reinterpret_cast<const f16x8*>(vrow + (size_t)(4 * u + lg) * D);
+      for (int u = 0; u < 4; ++u) o.v[j][u] = *reinterpret_cast<const f16x8*>(vrow + (size_t)(4 * u + lg) * D);
     }
-    // Keep all 32 loads ahead of their first use (the scheduler would otherwise
-    // interleave them with the MFMAs and leave one 1 KiB load in flight).
-    __builtin_amdgcn_sched_barrier(0);
+  };
+  auto compute_block = [&](const Blk& o, int blk) __attribute__((always_inline)) {
+    const int tb = blk * kBlock;
     // Scores: sc[j][r] = S[head 4*lg + r][token tb + 16*j + li].
-    f32x4 sc[4];
+    f32x4 sc[kTiles];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < kTiles; ++j) {
       f32x4 c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int s = 0; s < 4; ++s) c = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[s], kb[j][s], c, 0, 0, 0);
+      for (int s = 0; s < 4; ++s) c = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[s], o.k[j][s], c, 0, 0, 0);
       const bool valid = tb + 16 * j + li < L;
 #pragma unroll
       for (int r = 0; r < 4; ++r) sc[j][r] = valid ? c[r] * scale_log2 : -INFINITY;
@@ -139,14 +209,16 @@ __global__ __launch_bounds__(64 * kWaves) void attn_f16_d128(
     float alpha[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      float bm = fmaxf(fmaxf(sc[0][r], sc[1][r]), fmaxf(sc[2][r], sc[3][r]));
+      float bm = sc[0][r];
+#pragma unroll
+      for (int j = 1; j < kTiles; ++j) bm = fmaxf(bm, sc[j][r]);
 #pragma unroll
       for (int off = 1; off < 16; off <<= 1) bm = fmaxf(bm, __shfl_xor(bm, off, 64));
       const float mn = fmaxf(m[r], bm);  // finite: token tb is always visible
       alpha[r] = exp2f(m[r] - mn);
       float ps = 0.f;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+      for (int j = 0; j < kTiles; ++j) {
         const float p = exp2f(sc[j][r] - mn);
         sc[j][r] = p;
         ps += p;
@@ -162,13 +234,13 @@ __global__ __launch_bounds__(64 * kWaves) void attn_f16_d128(
       for (int e = 0; e < 8; ++e) acc[h][e] *= a;
     }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < kTiles; ++j) {
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const int tok = 4 * u + lg;
         float vf[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) vf[e] = static_cast<float>(vb[j][u][e]);
+        for (int e = 0; e < 8; ++e) vf[e] = static_cast<float>(o.v[j][u][e]);
 #pragma unroll
         for (int h = 0; h < G; ++h) {
           const float p = __shfl(sc[j][h & 3], tok + 16 * (h >> 2), 64);
@@ -177,6 +249,15 @@ __global__ __launch_bounds__(64 * kWaves) void attn_f16_d128(
         }
       }
     }
+  };
+
+  for (int blk = b0 + wave; blk < b1; blk += kWaves) {
+    Blk A;
+    load_block(A, blk);
+    // Keep all loads of the block ahead of their first use (the scheduler would
+    // otherwise interleave them with the MFMAs and leave one load in flight).
+    __builtin_amdgcn_sched_barrier(0);
+    compute_block(A, blk);
   }
 
   // Wavefront totals: O over the 4 token groups, l over the 16 lanes of a row.
@@ -345,10 +426,10 @@ int choose_splits(int rows, int Hkv, int max_context) {
 int launch_attention(const void* q, const void* k_pool, const void* v_pool, const int32_t* page_table,
                      const int32_t* seq_lens, void* out, void* workspace, size_t workspace_bytes,
                      int batch, int q_len, int Hq, int Hkv, int D, int P, int max_pages, float scale,
-                     int kv_dtype, void* stream) {
+                     int kv_dtype, void* stream, QkvIn qkv = QkvIn{nullptr, 0, nullptr, nullptr}) {
   CIR_CHECK_ARG(batch >= 0 && q_len >= 1, "attention: batch must be >= 0 and q_len >= 1");
   if (batch == 0) return 0;
-  CIR_CHECK_ARG(q && k_pool && v_pool && page_table && seq_lens && out, "attention: null pointer");
+  CIR_CHECK_ARG((q || qkv.part) && k_pool && v_pool && page_table && seq_lens && out, "attention: null pointer");
   CIR_CHECK_ARG(Hkv > 0 && Hq > 0 && Hq % Hkv == 0, "attention: num_heads (%d) must be a multiple of num_kv_heads (%d)", Hq, Hkv);
   CIR_CHECK_ARG(D > 0 && D <= 256, "attention: head_dim %d out of range (1..256)", D);
   CIR_CHECK_ARG(P > 0 && max_pages > 0, "attention: page_size and max_pages must be positive");
@@ -363,19 +444,22 @@ int launch_attention(const void* q, const void* k_pool, const void* v_pool, cons
   const int G = Hq / Hkv;
   hipStream_t s = as_stream(stream);
   const bool mfma = kv_dtype == CIR_F16 && D == 128 && P % 16 == 0 && G <= 8;
+  CIR_CHECK_ARG(!qkv.part || (mfma && q_len == 1 && qkv.splits >= 1 && qkv.inv_freq && qkv.positions),
+                "attention: the fused QKV input needs decode (q_len 1), fp16 pools, head_dim 128, page_size %% 16 == 0, "
+                "num_heads/num_kv_heads <= 8 and inv_freq/positions");
   const int S = mfma ? choose_splits(rows, Hkv, max_ctx) : generic_chunks(max_ctx);
   float* part_o = static_cast<float*>(workspace);
   float* part_ml = part_o + (size_t)rows * Hq * S * D;
   dim3 grid(S, Hkv, rows);
   if (mfma) {
     auto kq = static_cast<const f16*>(q);
-    auto kk = static_cast<const f16*>(k_pool);
-    auto kv = static_cast<const f16*>(v_pool);
+    auto kk = static_cast<f16*>(const_cast<void*>(k_pool));
+    auto kv = static_cast<f16*>(const_cast<void*>(v_pool));
     auto ko = static_cast<f16*>(out);
 #define CIR_ATT_CASE(g)                                                                                             \
   case g:                                                                                                           \
     attn_f16_d128<g><<<grid, 64 * kWaves, 0, s>>>(kq, kk, kv, page_table, seq_lens, ko, part_o, part_ml, q_len, Hq, \
-                                                  Hkv, P, max_pages, S, scale_log2);                                \
+                                                  Hkv, P, max_pages, S, scale_log2, qkv);                           \
     break;
     switch (G) {
       CIR_ATT_CASE(1) CIR_ATT_CASE(2) CIR_ATT_CASE(3) CIR_ATT_CASE(4)
@@ -435,3 +519,16 @@ extern "C" int cir_paged_prefill_attention(const void* q, const void* k_pool, co
                                q_len, num_heads, num_kv_heads, head_dim, page_size, max_pages, scale, kv_dtype,
                                stream);
 }
+
+extern "C" int cir_paged_decode_attention_qkv(const float* qkv_partial, int splits, const float* inv_freq,
+                                              const int32_t* positions, void* k_pool, void* v_pool,
+                                              const int32_t* page_table, const int32_t* seq_lens, void* out,
+                                              void* workspace, size_t workspace_bytes, int batch, int num_heads,
+                                              int num_kv_heads, int head_dim, int page_size, int max_pages,
+                                              float scale, void* stream) {
+  CIR_CHECK_ARG(batch == 0 || qkv_partial, "attention_qkv: null qkv_partial");
+  return cir::launch_attention(nullptr, k_pool, v_pool, page_table, seq_lens, out, workspace, workspace_bytes, batch,
+                               1, num_heads, num_kv_heads, head_dim, page_size, max_pages, scale, CIR_F16, stream,
+                               cir::QkvIn{qkv_partial, splits, inv_freq, positions});
+}
+

@@ -32,6 +32,8 @@ _SIGNATURES = {
     "cir_paged_attention_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int, _c_int]),
     "cir_paged_decode_attention": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_size, _c_int, _c_int, _c_int, _c_int,
                                             _c_int, _c_int, _c_float, _c_int, _vp]),
+    "cir_paged_decode_attention_qkv": (_c_int, [_vp, _c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_size, _c_int,
+                                                _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _vp]),
     "cir_paged_prefill_attention": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_size, _c_int, _c_int, _c_int, _c_int,
                                              _c_int, _c_int, _c_int, _c_float, _c_int, _vp]),
     "cir_qweight_tiled_bytes": (_c_size, [_c_int, _c_int, _c_int]),

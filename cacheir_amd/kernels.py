@@ -77,6 +77,37 @@ def paged_decode_attention(q, k_pool, v_pool, page_table, seq_lens, *, scale: fl
     return out
 
 
+def paged_decode_attention_qkv(part, inv_freq, positions, k_pool, v_pool, page_table, seq_lens, *, num_heads: int,
+                               scale: float | None = None, out: torch.Tensor | None = None,
+                               workspace: torch.Tensor | None = None, check_tables: bool = False) -> torch.Tensor:
+    """Decode attention fed by the QKV projection's fp32 partials ``[splits, B, (Hq + 2 Hkv) D]``: RoPE, the KV
+    append of the new token and attention in one launch (fp16 pools, head_dim 128). Returns out ``[B, Hq, D]``."""
+    _cuda(part, "part")
+    _req(part.dtype == torch.float32 and part.dim() == 3, "part must be float32 [splits, batch, n]", TypeError)
+    splits, batch, n = part.shape
+    _req(k_pool.dtype == torch.float16, "the fused QKV attention needs float16 pools", TypeError)
+    _, kvh, psize, hd = _check_pool(k_pool, k_pool, v_pool, page_table, seq_lens, num_heads, check_tables)
+    _req(n == (num_heads + 2 * kvh) * hd, "qkv partial width must be (num_heads + 2 kv_heads) * head_dim")
+    _req(page_table.shape[0] == batch and seq_lens.shape == (batch,), "shape mismatch")
+    _cuda(positions, "positions")
+    _cuda(inv_freq, "inv_freq")
+    _req(positions.dtype == torch.int32 and positions.numel() == batch, "positions must be int32 [batch]", TypeError)
+    _req(inv_freq.dtype == torch.float32 and inv_freq.numel() == hd // 2, "inv_freq must be float32 [D/2]", TypeError)
+    max_pages = page_table.shape[1]
+    if out is None:
+        out = torch.empty((batch, num_heads, hd), dtype=k_pool.dtype, device=k_pool.device)
+    _cuda(out, "out")
+    _req(out.shape == (batch, num_heads, hd) and out.dtype == k_pool.dtype, "out must be [batch, num_heads, head_dim]")
+    if workspace is None:
+        workspace = attention_workspace(batch, num_heads, hd, max_pages * psize, k_pool.device)
+    scale = 1.0 / math.sqrt(hd) if scale is None else scale
+    hip.call("cir_paged_decode_attention_qkv", part.data_ptr(), splits, inv_freq.data_ptr(), positions.data_ptr(),
+             k_pool.data_ptr(), v_pool.data_ptr(), page_table.data_ptr(), seq_lens.data_ptr(), out.data_ptr(),
+             workspace.data_ptr(), workspace.numel(), batch, num_heads, kvh, hd, psize, max_pages, float(scale),
+             hip.stream_handle())
+    return out
+
+
 def paged_prefill_attention(q, k_pool, v_pool, page_table, seq_lens, q_len: int, *, scale: float | None = None,
                             out=None, workspace=None, check_tables: bool = False) -> torch.Tensor:
     """q ``[B*q_len, Hq, D]``; ``seq_lens`` are lengths after appending the q_len tokens (causal)."""

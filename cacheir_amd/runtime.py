@@ -147,6 +147,14 @@ class StepPlan:
         self.attn_ws = torch.zeros(max(attn_need, 4), dtype=torch.uint8, device=dev)  # zeroed once; calls leave it zeroed
 
     # ------------------------------------------------------------------ build --
+    def _fuse_qkv_into_attention(self, users, k_pool: torch.Tensor, head_dim: int) -> bool:
+        """Decode steps whose q feeds only decode attention over fp16 pages (head_dim 128) run the QKV
+        epilogue inside the attention kernel (``cir_paged_decode_attention_qkv``)."""
+        cfg = self.rt.config
+        return (self.q_len == 1 and bool(users) and all(u.op == "paged_attention_decode" for u in users)
+                and k_pool.dtype == torch.float16 and self.rt.dtype == torch.float16 and head_dim == 128
+                and k_pool.shape[2] % 16 == 0 and cfg.num_attention_heads // cfg.num_key_value_heads <= 8)
+
     def _build(self, graph: Graph) -> None:
         rt, rows = self.rt, self.rows
         consumers = graph.consumers()
@@ -220,8 +228,14 @@ class StepPlan:
                 cfg = rt.config
                 hd = int(attrs.get("head_dim", cfg.head_dim))
                 inv = rt.inv_freq(hd, float(attrs.get("rope_theta", cfg.rope_theta)))
-                q_out = buf(cfg.num_attention_heads * hd, rt.dtype)
                 kp, vp = rt.kv_allocator.layer_pools(layer)
+                if self._fuse_qkv_into_attention(consumers.get(outs[0], []), kp, hd):
+                    # RoPE + KV append happen inside the decode attention kernel that consumes q
+                    env[outs[0]] = ("qkv-partials", part, inv, layer)
+                    env[outs[1]], env[outs[2]] = ("kv-appended", layer), ("kv-appended", layer)
+                    rt._count("rocm.rmsnorm_qkv")
+                    continue
+                q_out = buf(cfg.num_attention_heads * hd, rt.dtype)
                 self.launches.append(lambda part=part, inv=inv, q=q_out, kp=kp, vp=vp, hd=hd:
                                      kernels.epilogue_qkv_rope_append(
                                          part(), inv, self.positions, self.page_table, q, kp, vp, batch=self.batch,
@@ -235,9 +249,20 @@ class StepPlan:
                     raise NotImplementedError(
                         f"{node.name}: attention whose K/V are not produced by fused_rmsnorm_qkv_rope of layer {layer}")
                 heads, hd = int(attrs["num_heads"]), int(attrs["head_dim"])
-                q = as_dtype(env[ins[0]], rt.dtype)
                 out = buf(heads * hd, rt.dtype)
                 kp, vp = rt.kv_allocator.layer_pools(layer)
+                qin = env[ins[0]]
+                if isinstance(qin, tuple) and qin[0] == "qkv-partials":
+                    _, part, inv, _ = qin
+                    ov = out.view(rows, heads, hd)
+                    self.launches.append(lambda part=part, inv=inv, ov=ov, kp=kp, vp=vp, h=heads:
+                                         kernels.paged_decode_attention_qkv(
+                                             part(), inv, self.positions, kp, vp, self.page_table, self.seq_lens,
+                                             num_heads=h, out=ov, workspace=self.attn_ws))
+                    rt._count("rocm.rope_kv_append_paged_attention_decode")
+                    env[outs[0]] = out
+                    continue
+                q = as_dtype(qin, rt.dtype)
                 decode = op == "paged_attention_decode" and self.q_len == 1
                 qv, ov = q.view(rows, heads, hd), out.view(rows, heads, hd)
                 if decode:

@@ -56,6 +56,24 @@ int cir_paged_decode_attention(const void* q, const void* k_pool, const void* v_
                                int batch, int num_heads, int num_kv_heads, int head_dim,
                                int page_size, int max_pages, float scale, int kv_dtype, void* stream);
 
+/* Decode attention fused with the QKV epilogue: instead of a finished q it takes the
+ * QKV projection's fp32 split-k partials [splits][batch][(num_heads + 2 num_kv_heads)
+ * head_dim] (q | k | v columns, as cir_qgemm writes them), applies interleaved RoPE
+ * at positions[batch] to q and k (inv_freq[head_dim/2] fp32), appends k and v of the
+ * new token to its page, and attends as cir_paged_decode_attention does (seq_lens
+ * count the new token).  Results, including the pool contents, are bitwise those of
+ * cir_epilogue_qkv_rope_append followed by cir_paged_decode_attention.  fp16 pools,
+ * head_dim 128, page_size a multiple of 16, num_heads/num_kv_heads <= 8.
+ * Replaces the decode pair fused_rmsnorm_qkv_rope (RoPE + KV append part,
+ * cacheir/runtime/cpu.py:234-249,324-340, cuda.py:800-820) -> paged_attention_decode
+ * (cacheir/backends/triton_kernels.py:174-217, cuda.py:1183-1253). */
+int cir_paged_decode_attention_qkv(const float* qkv_partial, int splits, const float* inv_freq,
+                                   const int32_t* positions, void* k_pool, void* v_pool,
+                                   const int32_t* page_table, const int32_t* seq_lens, void* out,
+                                   void* workspace, size_t workspace_bytes, int batch, int num_heads,
+                                   int num_kv_heads, int head_dim, int page_size, int max_pages,
+                                   float scale, void* stream);
+
 /* Causal prefill over the same paged pool (reference prefill attention semantics,
  * cacheir/runtime/cpu.py:361-368): q is [batch * q_len, num_heads, head_dim]; row
  * (b, s) attends to tokens t < seq_lens[b] - q_len + s + 1, where seq_lens[b] is the

@@ -240,6 +240,46 @@ def test_epilogue_qkv_rope_append(device, kvdt):
             np.testing.assert_allclose(vpn[slot, :, off].reshape(-1), v_ref[s], rtol=tol, atol=tol)
 
 
+@pytest.mark.gpu
+@pytest.mark.parametrize("batch,hq,hkv,splits", [(32, 32, 8, 3), (2, 32, 8, 1), (5, 28, 4, 2), (3, 8, 8, 1)])
+def test_fused_qkv_decode_attention_matches_epilogue_then_attention(device, batch, hq, hkv, splits):
+    """cir_paged_decode_attention_qkv == cir_epilogue_qkv_rope_append + cir_paged_decode_attention, bitwise:
+    attention output and the pool contents (the appended k/v), incl. small batches that split the context."""
+    from cacheir_amd import kernels
+
+    rng = np.random.default_rng(batch * 100 + hq)
+    d, psize = 128, 16
+    lens = rng.integers(1, 700, batch).astype(np.int32)          # after the append
+    positions = (lens - 1).astype(np.int32)
+    pages = [-(-int(n) // psize) for n in lens]
+    max_pages = max(pages) + 1
+    slots = sum(pages) + 3
+    perm = rng.permutation(slots).astype(np.int32)
+    pt = np.zeros((batch, max_pages), np.int32)
+    o = 0
+    for b, n in enumerate(pages):
+        pt[b, :n] = perm[o:o + n]
+        o += n
+    n_cols = (hq + 2 * hkv) * d
+    part = rng.standard_normal((splits, batch, n_cols)).astype(np.float32)
+    inv = (1.0 / (500000.0 ** (np.arange(0, d // 2, dtype=np.float32) * 2.0 / d))).astype(np.float32)
+    kp0 = torch.randn((slots, hkv, psize, d), device=device).half()
+    vp0 = torch.randn((slots, hkv, psize, d), device=device).half()
+    P, I, POS, PT, L = (to_dev(a, device) for a in (part, inv, positions, pt, lens))
+
+    kp1, vp1 = kp0.clone(), vp0.clone()
+    q = torch.empty((batch, hq * d), dtype=torch.float16, device=device)
+    kernels.epilogue_qkv_rope_append(P, I, POS, PT, q, kp1, vp1, batch=batch, q_len=1, num_heads=hq,
+                                     num_kv_heads=hkv, head_dim=d)
+    ref = kernels.paged_decode_attention(q.view(batch, hq, d), kp1, vp1, PT, L)
+
+    kp2, vp2 = kp0.clone(), vp0.clone()
+    got = kernels.paged_decode_attention_qkv(P, I, POS, kp2, vp2, PT, L, num_heads=hq, check_tables=True)
+    torch.cuda.synchronize()
+    assert torch.equal(kp2, kp1) and torch.equal(vp2, vp1), "appended K/V differ"
+    assert torch.equal(got, ref), f"max |d| {(got.float() - ref.float()).abs().max().item()}"
+
+
 def test_row_kernels(device):
     from cacheir_amd import kernels
 

@@ -12,6 +12,7 @@ namespace cir {
 
 typedef _Float16 f16;
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
@@ -34,6 +35,15 @@ inline int launch_status() { return static_cast<int>(hipGetLastError()); }
 template <typename T> __device__ __forceinline__ float to_f32(T v);
 template <> __device__ __forceinline__ float to_f32<float>(float v) { return v; }
 template <> __device__ __forceinline__ float to_f32<f16>(f16 v) { return static_cast<float>(v); }
+
+// Materialise v as an fp32 value: stops the compiler contracting the operation that
+// produced it with a following conversion (e.g. a multiply and an fp16 conversion
+// into one mixed-precision FMA, which rounds once instead of twice), so every kernel
+// that computes the same expression stores the same bits.
+__device__ __forceinline__ float as_f32_value(float v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
 
 template <typename T> __device__ __forceinline__ T from_f32(float v);
 template <> __device__ __forceinline__ float from_f32<float>(float v) { return v; }

@@ -264,11 +264,17 @@ struct XsChunk {  // this thread's share of one quad of activations
   u32x4 v[MT];
 };
 
-template <int FMT, int NT, int MT, int DW>
+// EPI 0: store fp32 split-k partials part[split][m][n].
+// EPI 1 (SwiGLU, one split): the weight tiles alternate gate / up (tile 2c = gate
+// rows 16c.., tile 2c+1 = the matching up rows), so a wavefront with NT = 2 holds
+// both accumulators of 16 intermediate columns and writes silu(g) * u to
+// out[m][N/2] (type TO) -- the SwiGLU of cpu.py:266-279 without a partials pass.
+template <int FMT, int NT, int MT, int DW, int EPI = 0, typename TO = float>
 __global__ __launch_bounds__(256) void qgemm_xs_kernel(const f16* __restrict__ x, int ldx,
                                                        const uint8_t* __restrict__ wq, const uint16_t* __restrict__ wd,
                                                        float* __restrict__ part, int M, int N, int K,
-                                                       int quads_per_split) {
+                                                       int quads_per_split, TO* __restrict__ act = nullptr) {
+  static_assert(EPI == 0 || NT == 2, "the SwiGLU epilogue pairs tile 2c (gate) with 2c+1 (up)");
   constexpr int LB = Stage<FMT, NT, MT>::LB;
   __shared__ __align__(16) uint8_t xs[2][16 * MT * kXsRowBytes];
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -377,19 +383,42 @@ __global__ __launch_bounds__(256) void qgemm_xs_kernel(const f16* __restrict__ x
     }
   });
 
+  if constexpr (EPI == 1) {
+    const int inter = N / 2;
+    const int col = (nt0 >> 1) * 16 + li;
+    if (nt0 + 1 < NTILES && col < inter) {
 #pragma unroll
-  for (int a = 0; a < MT; ++a)
-#pragma unroll
-    for (int b = 0; b < NT; ++b) {
-      const int n = (nt0 + b) * 16 + li;
-      if (nt0 + b < NTILES && n < N) {
+      for (int a = 0; a < MT; ++a)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int m = m0 + 16 * a + 4 * lg + r;
-          if (m < M) part[((size_t)split * M + m) * N + n] = acc[a][b][r];
+          const float g = acc[a][0][r], u = acc[a][1][r];
+          if (m < M) act[(size_t)m * inter + col] = static_cast<TO>(as_f32_value((g / (1.0f + expf(-g))) * u));
+        }
+    }
+  } else {
+#pragma unroll
+    for (int a = 0; a < MT; ++a)
+#pragma unroll
+      for (int b = 0; b < NT; ++b) {
+        const int n = (nt0 + b) * 16 + li;
+        if (nt0 + b < NTILES && n < N) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int m = m0 + 16 * a + 4 * lg + r;
+            if (m < M) part[((size_t)split * M + m) * N + n] = acc[a][b][r];
+          }
         }
       }
-    }
+  }
+}
+
+template <int FMT, int MT, typename TO>
+void launch_qgemm_swiglu(const f16* x, int ldx, const uint8_t* wq, const uint16_t* wd, TO* act, int M, int N, int K,
+                         hipStream_t s) {
+  const int NTILES = (N + 15) / 16;
+  dim3 grid((NTILES + 7) / 8, 1, (M + 16 * MT - 1) / (16 * MT));
+  qgemm_xs_kernel<FMT, 2, MT, 4, 1, TO><<<grid, 256, 0, s>>>(x, ldx, wq, wd, nullptr, M, N, K, K / 128, act);
 }
 
 template <int FMT, int NT, int MT, int DW>
@@ -499,6 +528,37 @@ extern "C" int cir_qgemm(const void* x, int ldx, const void* w_tiled, int fmt, f
   } else {
     dispatch_qgemm<CIR_Q8_0>(xh, ldx, q, d, y_partial, m, n, k, splits, s);
   }
+  return launch_status();
+}
+
+extern "C" int cir_qgemm_swiglu(const void* x, int ldx, const void* w_tiled, int fmt, void* out, int odt, int m,
+                                int inter, int k, void* stream) {
+  CIR_CHECK_ARG(fmt == CIR_Q4_0 || fmt == CIR_Q8_0, "qgemm_swiglu: fmt must be CIR_Q4_0 or CIR_Q8_0 (got %d)", fmt);
+  CIR_CHECK_ARG(odt == CIR_F16 || odt == CIR_F32, "qgemm_swiglu: out dtype must be CIR_F16 or CIR_F32");
+  CIR_CHECK_ARG(m >= 0 && inter >= 0 && k >= 0, "qgemm_swiglu: negative size");
+  if (m == 0 || inter == 0) return 0;
+  CIR_CHECK_ARG(inter % 16 == 0, "qgemm_swiglu: intermediate size (%d) must be a multiple of 16", inter);
+  CIR_CHECK_ARG(k > 0 && k % 128 == 0, "qgemm_swiglu: k (%d) must be a positive multiple of 128", k);
+  CIR_CHECK_ARG(ldx >= k && ldx % 8 == 0, "qgemm_swiglu: ldx (%d) must be >= k and a multiple of 8", ldx);
+  CIR_CHECK_ARG(x && w_tiled && out, "qgemm_swiglu: null pointer");
+  CIR_CHECK_ARG((m + 15) / 16 <= 65535, "qgemm_swiglu: grid too large");
+  const int n = 2 * inter;
+  const size_t tiles = (size_t)(n / 16) * (k / 128);
+  const uint8_t* q = static_cast<const uint8_t*>(w_tiled);
+  const uint16_t* d = reinterpret_cast<const uint16_t*>(q + tiles * 64 * quant_bytes_per_lane(fmt));
+  const f16* xh = static_cast<const f16*>(x);
+  hipStream_t s = as_stream(stream);
+  auto go = [&]<int FMT>() {
+    if (odt == CIR_F16) {
+      if (m <= 16) launch_qgemm_swiglu<FMT, 1>(xh, ldx, q, d, static_cast<f16*>(out), m, n, k, s);
+      else launch_qgemm_swiglu<FMT, 2>(xh, ldx, q, d, static_cast<f16*>(out), m, n, k, s);
+    } else {
+      if (m <= 16) launch_qgemm_swiglu<FMT, 1>(xh, ldx, q, d, static_cast<float*>(out), m, n, k, s);
+      else launch_qgemm_swiglu<FMT, 2>(xh, ldx, q, d, static_cast<float*>(out), m, n, k, s);
+    }
+  };
+  if (fmt == CIR_Q4_0) go.template operator()<CIR_Q4_0>();
+  else go.template operator()<CIR_Q8_0>();
   return launch_status();
 }
 

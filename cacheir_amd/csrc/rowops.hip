@@ -99,6 +99,17 @@ __device__ __forceinline__ float4 split_sum4(const float* __restrict__ part, int
   return t;
 }
 
+// Four consecutive values as one vector access (8 B for fp16, 16 B for fp32).
+__device__ __forceinline__ float4 load4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+__device__ __forceinline__ float4 load4(const f16* p) {
+  const f16x4 h = *reinterpret_cast<const f16x4*>(p);
+  return make_float4((float)h[0], (float)h[1], (float)h[2], (float)h[3]);
+}
+__device__ __forceinline__ void store4(float* p, float4 v) { *reinterpret_cast<float4*>(p) = v; }
+__device__ __forceinline__ void store4(f16* p, float4 v) {
+  *reinterpret_cast<f16x4*>(p) = f16x4{(f16)v.x, (f16)v.y, (f16)v.z, (f16)v.w};
+}
+
 // Residual epilogue + RMSNorm of the result, one workgroup per row, 4 columns per
 // thread per step: h = residual + sum of partials (fp32, to h_out) and
 // xn = (h * rsqrt(mean(h^2) + eps)) * w.  N % 4 == 0 and N <= 8192.
@@ -125,17 +136,20 @@ __global__ __launch_bounds__(kRowThreads) void residual_rmsnorm_kernel(
     v[i] = t;
     ss += t.x * t.x + t.y * t.y + t.z * t.z + t.w * t.w;
   }
+  // The norm weights do not depend on the sum: load them before the reduction.
+  float4 wv[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int c = 4 * (threadIdx.x + i * kRowThreads);
+    wv[i] = c < N ? load4(w + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
   const float scale = 1.0f / sqrtf(block_sum_1024(ss, scratch) / (float)N + eps);
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int c = 4 * (threadIdx.x + i * kRowThreads);
-    if (c < N) {
-      TO* o = xn + (size_t)r * N + c;
-      o[0] = from_f32<TO>((v[i].x * scale) * to_f32(w[c]));
-      o[1] = from_f32<TO>((v[i].y * scale) * to_f32(w[c + 1]));
-      o[2] = from_f32<TO>((v[i].z * scale) * to_f32(w[c + 2]));
-      o[3] = from_f32<TO>((v[i].w * scale) * to_f32(w[c + 3]));
-    }
+    if (c < N)
+      store4(xn + (size_t)r * N + c, make_float4((v[i].x * scale) * wv[i].x, (v[i].y * scale) * wv[i].y,
+                                                 (v[i].z * scale) * wv[i].z, (v[i].w * scale) * wv[i].w));
   }
 }
 
@@ -178,7 +192,7 @@ __global__ void epi_store_kernel(const float* __restrict__ part, int splits, con
   out[i + 3] = from_f32<T>(v.w);
 }
 
-__device__ __forceinline__ float silu_mul1(float g, float u) { return (g / (1.0f + expf(-g))) * u; }
+__device__ __forceinline__ float silu_mul1(float g, float u) { return as_f32_value((g / (1.0f + expf(-g))) * u); }
 
 // SwiGLU over [gate | up] partial columns, 4 outputs per thread (I % 4 == 0).
 template <int SMAX, typename T>

@@ -196,6 +196,29 @@ def qgemm_partial(x: torch.Tensor, w: QWeight, splits: int | None = None, out: t
     return out.view(-1)[: splits * m * w.n].view(splits, m, w.n)
 
 
+def interleave_gate_up(gate_blocks: torch.Tensor, up_blocks: torch.Tensor, rows: int) -> torch.Tensor:
+    """GGUF block rows of gate and up ([rows, row_bytes] each, uint8) -> [2*rows, row_bytes] in the order
+    gate 16c..16c+15, up 16c..16c+15, c = 0, 1, ... (the tile pairing ``cir_qgemm_swiglu`` reads)."""
+    _req(rows % 16 == 0, "gate/up rows must be a multiple of 16")
+    g = gate_blocks.reshape(rows // 16, 1, 16, -1)
+    u = up_blocks.reshape(rows // 16, 1, 16, -1)
+    return torch.cat([g, u], dim=1).reshape(2 * rows, -1).contiguous()
+
+
+def qgemm_swiglu(x: torch.Tensor, w: QWeight, out_dtype: torch.dtype = torch.float16, out=None) -> torch.Tensor:
+    """``silu(x @ gate^T) * (x @ up^T)`` from the interleaved gate|up tiled weight (``interleave_gate_up``)."""
+    _cuda(x, "x", rows_only=True)
+    _req(x.dtype == torch.float16, "qgemm activations must be float16", TypeError)
+    _req(x.dim() == 2 and x.shape[1] == w.k and w.n % 32 == 0, f"x must be [m, {w.k}] and n a multiple of 32")
+    m, inter = x.shape[0], w.n // 2
+    if out is None:
+        out = torch.empty((m, inter), dtype=out_dtype, device=x.device)
+    _req(out.shape == (m, inter) and out.is_contiguous(), "out must be [m, n/2] contiguous")
+    hip.call("cir_qgemm_swiglu", x.data_ptr(), x.stride(0), w.tiled.data_ptr(), w.fmt, out.data_ptr(),
+             hip.dtype_code(out.dtype), m, inter, w.k, hip.stream_handle())
+    return out
+
+
 def gemm_f32_partial(x: torch.Tensor, w: torch.Tensor, splits: int = 1, out=None) -> torch.Tensor:
     _cuda(x, "x")
     _cuda(w, "w")

@@ -13,6 +13,12 @@ once); a session's slots are shared by all layers because every layer appends th
 same token positions, so one page table serves the whole step; K/V are written
 in place by the QKV epilogue kernel (no ``torch.cat`` of the whole cache and no
 page re-write, cf. ``cuda.py:322-334,172-199``).
+
+Shared prefixes alias pages instead of copying them (the reference restores a
+prefix from a host snapshot, ``kv_cache.py:262-307``, ``cuda.py:336-355``): slots
+are reference counted, a session that reuses a cached prefix points its page table
+at the prefix's slots, and a page is copied (for every layer) only when a session
+is about to write into a page someone else still references (copy on write).
 """
 from __future__ import annotations
 
@@ -36,10 +42,11 @@ class HipKVPageAllocator:
         self.capacity = 0
         self.k = self.v = None
         self._free: list[int] = []
-        self._owner_of: dict[int, str] = {}
+        self._refs: dict[int, int] = {}  # slot -> number of page tables (and prefix-cache entries) using it
         self.pool_grows = 0
         self.allocated_pages_total = 0
         self.released_pages = 0
+        self.copied_pages = 0
         self.generation = 0  # bumps when the pool tensors are re-allocated
         self._grow(max(1, int(capacity_pages)))
 
@@ -63,21 +70,45 @@ class HipKVPageAllocator:
     def new_owner(self) -> str:
         return f"hip-session-{next(self._owners)}"
 
-    def allocate(self, owner: str) -> int:
-        if self.max_resident_pages is not None and len(self._owner_of) >= self.max_resident_pages:
+    def allocate(self, owner: str = "") -> int:
+        if self.max_resident_pages is not None and len(self._refs) >= self.max_resident_pages:
             raise RuntimeError(f"KV page budget exhausted ({self.max_resident_pages} resident pages)")
         if not self._free:
             self._grow(self.capacity * 2)
         slot = self._free.pop()
-        self._owner_of[slot] = owner
+        self._refs[slot] = 1
         self.allocated_pages_total += 1
         return slot
 
-    def release(self, slots: list[int]) -> None:
+    def share(self, slots: list[int]) -> None:
+        """One more user of each of ``slots`` (all must be allocated)."""
         for s in slots:
-            if self._owner_of.pop(s, None) is not None:
+            if s not in self._refs:
+                raise ValueError(f"slot {s} is not allocated")
+        for s in slots:
+            self._refs[s] += 1
+
+    def refcount(self, slot: int) -> int:
+        return self._refs.get(slot, 0)
+
+    def release(self, slots: list[int]) -> None:
+        """Drop one use of each slot; a slot nobody uses any more returns to the free list."""
+        for s in slots:
+            n = self._refs.get(s)
+            if n is None:
+                continue
+            if n > 1:
+                self._refs[s] = n - 1
+            else:
+                del self._refs[s]
                 self._free.append(s)
                 self.released_pages += 1
+
+    def copy_page(self, src: int, dst: int) -> None:
+        """K and V of page ``src`` into ``dst`` for every layer (device copies, stream ordered)."""
+        self.k[:, dst].copy_(self.k[:, src])
+        self.v[:, dst].copy_(self.v[:, src])
+        self.copied_pages += 1
 
     def layer_pools(self, layer: int) -> tuple[torch.Tensor, torch.Tensor]:
         return self.k[layer], self.v[layer]
@@ -91,13 +122,15 @@ class HipKVPageAllocator:
             "page_size": self.page_size,
             "page_bytes": self.page_bytes,
             "allocated_pages_total": self.allocated_pages_total,
-            "resident_pages": len(self._owner_of),
+            "resident_pages": len(self._refs),
+            "shared_pages": sum(1 for n in self._refs.values() if n > 1),
+            "copied_pages": self.copied_pages,
             "released_pages": self.released_pages,
             "max_resident_pages": self.max_resident_pages,
             "pool_grows": self.pool_grows,
             "persistent_pools": [{
                 "layers": self.num_layers, "device": str(self.device), "dtype": str(self.dtype),
-                "kv_heads": self.kv_heads, "head_dim": self.head_dim, "slots": len(self._owner_of),
+                "kv_heads": self.kv_heads, "head_dim": self.head_dim, "slots": len(self._refs),
                 "capacity": self.capacity,
                 "bytes": int(self.k.numel() * self.k.element_size() * 2),
             }],
@@ -128,9 +161,28 @@ class HipPagedKVCache:
         return self.tokens if layer in self else 0
 
     def ensure_capacity(self, total_tokens: int) -> None:
+        """Own every page that tokens ``self.tokens .. total_tokens - 1`` will be written to: copy a page still
+        shared with another page table (copy on write), then allocate the missing pages."""
         need = -(-total_tokens // self.page_size)
+        for i in range(self.tokens // self.page_size, min(need, len(self.slots))):
+            old = self.slots[i]
+            if self.allocator.refcount(old) > 1:
+                new = self.allocator.allocate(self.owner)
+                self.allocator.copy_page(old, new)
+                self.allocator.release([old])
+                self.slots[i] = new
         while len(self.slots) < need:
             self.slots.append(self.allocator.allocate(self.owner))
+
+    def alias_prefix(self, slots: list[int], tokens: int) -> None:
+        """Drop this cache's pages and reuse the first ``tokens`` tokens held by ``slots`` (no copy)."""
+        pages = -(-tokens // self.page_size)
+        if pages > len(slots):
+            raise ValueError(f"{tokens} tokens need {pages} pages, got {len(slots)}")
+        self.clear()
+        self.slots = list(slots[:pages])
+        self.allocator.share(self.slots)
+        self.tokens = int(tokens)
 
     def clear(self) -> None:
         self.allocator.release(self.slots)

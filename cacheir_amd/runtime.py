@@ -29,6 +29,7 @@ from __future__ import annotations
 import itertools
 import json
 from collections import OrderedDict
+from dataclasses import dataclass
 from pathlib import Path
 from typing import Any, Iterable
 
@@ -87,11 +88,26 @@ class ByteTokenizer:
         return "".join(chr(v) if 32 <= v <= 126 else f"<{v}>" for v in (int(i) % self.vocab_size for i in ids))
 
 
-class PrefixCache:
-    """LRU map ``token prefix -> page snapshot`` (``cacheir/runtime/kv_cache.py:262-307``).
+@dataclass
+class PrefixPages:
+    """A cached prefix: the slots holding its K/V (one reference held by the cache) and its length."""
 
-    A snapshot holds device copies of the prefix's pages for every layer, so a hit
-    restores the KV of a prompt without recomputing it."""
+    allocator: HipKVPageAllocator
+    slots: list[int]
+    tokens: int
+
+    def release(self) -> None:
+        self.allocator.release(self.slots)
+        self.slots = []
+
+
+class PrefixCache:
+    """LRU map ``token prefix -> pages`` (``cacheir/runtime/kv_cache.py:262-307`` semantics).
+
+    The reference stores host snapshots of a prefix's KV and copies them back into a
+    new session.  Here an entry holds a reference to the prefix's device pages and a
+    hit aliases them into the new session's page table (``HipPagedKVCache.alias_prefix``):
+    no copy, and sequences that share a prompt prefix read the same pages."""
 
     def __init__(self, capacity: int = 8):
         self.capacity = max(1, int(capacity))
@@ -100,10 +116,14 @@ class PrefixCache:
 
     def put(self, token_ids, snapshot) -> None:
         key = tuple(int(t) for t in token_ids)
-        self._entries.pop(key, None)
+        old = self._entries.pop(key, None)
+        if old is not None and hasattr(old, "release"):
+            old.release()
         self._entries[key] = snapshot
         while len(self._entries) > self.capacity:
-            self._entries.popitem(last=False)
+            _, ev = self._entries.popitem(last=False)
+            if hasattr(ev, "release"):
+                ev.release()
             self.evictions += 1
 
     def longest_prefix(self, token_ids):
@@ -118,6 +138,12 @@ class PrefixCache:
         else:
             self.misses += 1
         return best, value
+
+    def clear(self) -> None:
+        for v in self._entries.values():
+            if hasattr(v, "release"):
+                v.release()
+        self._entries.clear()
 
     def stats(self) -> dict[str, int]:
         return {"capacity": self.capacity, "entries": len(self._entries), "hits": self.hits, "misses": self.misses,
@@ -324,9 +350,19 @@ class StepPlan:
                 self.launches.append(lambda x=x, w=w, o=out, e=eps: kernels.rmsnorm(x, w, e, o.dtype, out=o))
                 env[outs[0]] = out
             elif op in _SWIGLU_OPS:
+                odt = input_dtype_for(outs[0]) or torch.float32
+                inter = rt.weights._rows(ins[1])
+                if rt.weights.is_blocked((ins[1], ins[2])) and inter % 16 == 0:
+                    # gate|up GEMM with the SwiGLU applied in registers (interleaved gate/up tiles)
+                    W = rt.weights.swiglu_weight(ins[1], ins[2])
+                    x = as_dtype(env[ins[0]], torch.float16)
+                    out = buf(inter, odt)
+                    self.launches.append(lambda x=x, w=W, o=out: kernels.qgemm_swiglu(x, w, o.dtype, out=o))
+                    rt._count("rocm.qgemm_swiglu")
+                    env[outs[0]] = out
+                    continue
                 W = rt.weights.matmul_weight((ins[1], ins[2]))
                 part, _, n2 = gemm(env[ins[0]], W)
-                odt = input_dtype_for(outs[0]) or torch.float32
                 out = buf(n2 // 2, odt)
                 self.launches.append(lambda part=part, o=out: kernels.epilogue_swiglu(part(), o.dtype, out=o))
                 rt._count("rocm.swiglu_epilogue")
@@ -582,9 +618,34 @@ class HipRuntime:
         return out
 
     def prefill_tokens(self, token_ids, *, use_prefix_cache: bool = False, remember_prefix: bool = False):
+        """``cpu.py:140-165``: with ``use_prefix_cache`` the longest cached prefix of ``token_ids`` is reused
+        (its pages aliased, not copied) and only the rest is prefilled; returns (logits of the prefilled
+        tokens, the reused prefix)."""
         ids = [int(t) for t in token_ids]
-        logits = self.run([ids], mode="prefill", reset_kv=True)
-        return logits, ()
+        reused: tuple[int, ...] = ()
+        if use_prefix_cache and ids:
+            prefix, pages = self.prefix_cache.longest_prefix(ids)
+            if pages is not None and 0 < len(prefix) < len(ids) and pages.allocator is self.kv_allocator:
+                self.kv_cache.alias_prefix(pages.slots, len(prefix))
+                reused = tuple(prefix)
+                logits = self.run([ids[len(prefix):]], mode="prefill", reset_kv=False)
+            else:
+                logits = self.run([ids], mode="prefill", reset_kv=True)
+        else:
+            logits = self.run([ids], mode="prefill", reset_kv=True)
+        if remember_prefix and ids:
+            self.remember_prefix(ids)
+        return logits, reused
+
+    def remember_prefix(self, token_ids) -> None:
+        """Cache this session's pages as the KV of ``token_ids`` (the tokens it holds now)."""
+        ids = [int(t) for t in token_ids]
+        if len(ids) != self.kv_cache.tokens:
+            raise ValueError(f"remember_prefix: the session holds {self.kv_cache.tokens} tokens, not {len(ids)}")
+        pages = -(-len(ids) // self.kv_allocator.page_size)
+        slots = list(self.kv_cache.slots[:pages])
+        self.kv_allocator.share(slots)
+        self.prefix_cache.put(ids, PrefixPages(self.kv_allocator, slots, len(ids)))
 
     def generate_ids(self, prompt_ids, max_new_tokens: int = 16) -> list[int]:
         logits = self.run([list(prompt_ids)], mode="prefill", reset_kv=True)
@@ -598,7 +659,8 @@ class HipRuntime:
     def generate(self, prompt: str, *, max_new_tokens: int = 16, use_prefix_cache: bool = False,
                  remember_prefix: bool = True):
         ids = self.tokenizer.encode(prompt)
-        logits, _ = self.prefill_tokens(ids)
+        logits, _ = self.prefill_tokens(ids, use_prefix_cache=use_prefix_cache,
+                                        remember_prefix=remember_prefix and use_prefix_cache)
         for _ in range(max_new_tokens):
             nxt = int(torch.argmax(logits[0, -1]).item()) % self.config.vocab_size
             yield self.tokenizer.decode([nxt])

@@ -277,6 +277,20 @@ class HipWeightStore:
         self._packed[names] = w
         return w
 
+    def swiglu_weight(self, gate: str, up: str) -> "kernels.QWeight":
+        """Gate and up block weights as one tiled weight with their 16-row tiles interleaved (gate c, up c, ...),
+        the layout ``cir_qgemm_swiglu`` reads."""
+        key = (gate, up, "swiglu")
+        if key not in self._packed:
+            (gb, gf, rows, k), (ub, uf, rows_u, ku) = self._blocks(gate), self._blocks(up)
+            if gf != uf or k != ku or rows != rows_u:
+                raise ValueError(f"cannot pair {gate} and {up}: shapes or block formats differ")
+            inter = kernels.interleave_gate_up(gb.reshape(rows, -1), ub.reshape(rows, -1), rows)
+            self._packed[key] = kernels.QWeight.from_blocks(inter.reshape(-1), CIR_Q4_0 if gf == GGML_Q4_0 else CIR_Q8_0,
+                                                            2 * rows, k)
+            del gb, ub, inter
+        return self._packed[key]
+
     def _rows(self, name: str) -> int:
         return int(self.specs[name].tensor_type.shape[0])
 

@@ -114,6 +114,17 @@ size_t cir_qgemm_workspace_bytes(int m, int n, int splits);
 int cir_qgemm(const void* x, int ldx, const void* w_tiled, int fmt, float* y_partial,
               int m, int n, int k, int splits, void* stream);
 
+/* Gate|up projection fused with SwiGLU (cacheir/runtime/cpu.py:266-279,
+ * cuda.py:859-871 quantized_fused_swiglu): out[m][j] = silu(g) * u with g, u the
+ * projections of x onto gate row j and up row j, fp32 accumulate, one launch, no
+ * partials.  w_tiled is the tiled copy of the 2*inter rows in *interleaved* order --
+ * gate rows 16c..16c+15, then up rows 16c..16c+15, for c = 0, 1, ... (make it by
+ * permuting the GGUF block rows before cir_qweight_repack).  out dtype odt
+ * (CIR_F16 / CIR_F32), [m][inter].  inter % 16 == 0, k % 128 == 0.  Bitwise equal to
+ * cir_qgemm (splits 1) over the same tiles followed by cir_epilogue_swiglu. */
+int cir_qgemm_swiglu(const void* x, int ldx, const void* w_tiled, int fmt, void* out, int odt, int m,
+                     int inter, int k, void* stream);
+
 /* Dense weights W[n][k] in fp32 (x fp32) -- the fp32 parity path for unquantized
  * artifacts.  Writes y_partial[split][m][n]; splits must divide ceil(k/256). */
 int cir_gemm_f32(const float* x, int ldx, const float* w, float* y_partial,

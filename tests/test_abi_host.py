@@ -5,6 +5,7 @@ import subprocess
 from pathlib import Path
 
 import numpy as np
+import torch
 import pytest
 
 from cacheir_amd import hip
@@ -110,3 +111,71 @@ def test_host_quantizer_matches_oracle_decode(fmt):
     wm = np.take_along_axis(w.reshape(16, -1, 32), i[..., None], -1)
     dm = np.take_along_axis(dec.reshape(16, -1, 32), i[..., None], -1)
     np.testing.assert_allclose(dm, wm, rtol=2.0 ** -10)
+
+
+# ------------------------------------------------------------------ KV pages (host logic, CPU tensors) --
+def _alloc(pages=4):
+    from cacheir_amd.kv import HipKVPageAllocator
+
+    return HipKVPageAllocator(num_layers=2, kv_heads=1, head_dim=4, page_size=4, dtype=torch.float32, device="cpu",
+                              capacity_pages=pages)
+
+
+def test_kv_pages_refcount_alias_and_copy_on_write():
+    from cacheir_amd.kv import HipPagedKVCache
+
+    a = _alloc()
+    src = HipPagedKVCache(a)
+    src.ensure_capacity(6)  # 2 pages, the second half full
+    src.tokens = 6
+    for i, slot in enumerate(src.slots):
+        a.k[:, slot] = float(i + 1)
+        a.v[:, slot] = float(-(i + 1))
+    dst = HipPagedKVCache(a)
+    dst.alias_prefix(src.slots, 6)
+    assert dst.slots == src.slots and dst.tokens == 6
+    assert all(a.refcount(s) == 2 for s in src.slots)
+    # dst appends token 6: it lands in page 1, still shared -> copied; page 0 stays aliased
+    dst.ensure_capacity(7)
+    assert dst.slots[0] == src.slots[0] and dst.slots[1] != src.slots[1]
+    assert a.refcount(src.slots[0]) == 2 and a.refcount(src.slots[1]) == 1 and a.refcount(dst.slots[1]) == 1
+    assert torch.equal(a.k[:, dst.slots[1]], a.k[:, src.slots[1]]) and a.copied_pages == 1
+    a.k[:, dst.slots[1], :, 2] = 99.0  # the writer's copy changes, the source page does not
+    assert float(a.k[0, src.slots[1], 0, 2, 0]) == 2.0
+    # a page-aligned prefix needs no copy: new tokens go to new pages
+    dst2 = HipPagedKVCache(a)
+    dst2.alias_prefix(src.slots, 4)
+    dst2.ensure_capacity(5)
+    assert dst2.slots[0] == src.slots[0] and len(dst2.slots) == 2 and dst2.slots[1] not in src.slots
+    # releasing every user frees the pages
+    before = len(a._free)
+    for c in (dst, dst2, src):
+        c.clear()
+    assert a.stats()["resident_pages"] == 0 and len(a._free) == before + 4
+
+
+def test_prefix_cache_holds_and_releases_pages():
+    from cacheir_amd.kv import HipPagedKVCache
+    from cacheir_amd.runtime import PrefixCache, PrefixPages
+
+    a = _alloc()
+    s = HipPagedKVCache(a)
+    s.ensure_capacity(8)
+    s.tokens = 8
+    pc = PrefixCache(capacity=1)
+    a.share(s.slots)
+    pc.put(list(range(8)), PrefixPages(a, list(s.slots), 8))
+    s.clear()  # the cache still holds the pages
+    assert a.stats()["resident_pages"] == 2
+    key, pages = pc.longest_prefix(list(range(10)))
+    assert key == tuple(range(8)) and pages.tokens == 8 and pc.hits == 1
+    assert pc.longest_prefix([5, 6])[1] is None and pc.misses == 1
+    s2 = HipPagedKVCache(a)
+    s2.ensure_capacity(4)
+    s2.tokens = 4
+    a.share(s2.slots)
+    pc.put([1, 2, 3, 4], PrefixPages(a, list(s2.slots), 4))  # evicts the first entry (capacity 1)
+    assert pc.evictions == 1 and a.stats()["resident_pages"] == 1
+    pc.clear()
+    s2.clear()
+    assert a.stats()["resident_pages"] == 0

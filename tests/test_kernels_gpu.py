@@ -280,6 +280,106 @@ def test_fused_qkv_decode_attention_matches_epilogue_then_attention(device, batc
     assert torch.equal(got, ref), f"max |d| {(got.float() - ref.float()).abs().max().item()}"
 
 
+@pytest.mark.gpu
+@pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
+@pytest.mark.parametrize("m", [1, 8, 32])
+def test_qgemm_swiglu_matches_gemm_then_epilogue(device, fmt, m):
+    """cir_qgemm_swiglu over interleaved gate/up tiles == cir_qgemm (splits 1) + cir_epilogue_swiglu, bitwise,
+    and within the fp16 bound of the fp64 oracle."""
+    from cacheir_amd import kernels
+
+    rng = np.random.default_rng(11 + m)
+    inter, k = 160, 512
+    enc = quant.random_q4_0 if fmt == "q4_0" else quant.random_q8_0
+    dec = quant.decode_q4_0 if fmt == "q4_0" else quant.decode_q8_0
+    code = kernels.FMT_NAMES[fmt]
+    gate, up = enc(rng, inter, k)[0], enc(rng, inter, k)[0]
+    x = rng.standard_normal((m, k)).astype(np.float16)
+    xd = to_dev(x, device)
+    g_dev, u_dev = to_dev(gate, device), to_dev(up, device)
+    w_cat = kernels.QWeight.from_blocks(torch.cat([g_dev.reshape(-1), u_dev.reshape(-1)]), code, 2 * inter, k)
+    part = kernels.qgemm_partial(xd, w_cat, splits=1)
+    ref = kernels.epilogue_swiglu(part, torch.float16)
+    w_il = kernels.QWeight.from_blocks(kernels.interleave_gate_up(g_dev, u_dev, inter).reshape(-1), code, 2 * inter, k)
+    got = kernels.qgemm_swiglu(xd, w_il, torch.float16)
+    torch.cuda.synchronize()
+    assert torch.equal(got, ref)
+    xf = x.astype(np.float64)
+    g64, u64 = xf @ dec(gate, k).astype(np.float64).T, xf @ dec(up, k).astype(np.float64).T
+    want = g64 / (1.0 + np.exp(-g64)) * u64
+    err = np.abs(got.double().cpu().numpy() - want) - (2e-3 + 1e-2 * np.abs(want))
+    assert np.all(err <= 0), err.max()
+
+
+def _shared_prefix_case(device, rng, batch, prefix_pages, suffix_lo, suffix_hi, hkv=4, d=128, psize=16):
+    """BASELINE config 5 layout: every sequence's first ``prefix_pages`` pages are the same slots; suffix pages
+    are distinct and permuted.  Returns pools (torch fp16), page table, lengths and the slot count."""
+    suffix = rng.integers(suffix_lo, suffix_hi + 1, batch)
+    lens = prefix_pages * psize + suffix
+    spages = -(-suffix // psize)
+    slots = prefix_pages + int(spages.sum())
+    perm = rng.permutation(slots).astype(np.int32)
+    shared = perm[:prefix_pages]
+    max_pages = prefix_pages + int(spages.max())
+    pt = np.zeros((batch, max_pages), np.int32)
+    o = prefix_pages
+    for b in range(batch):
+        pt[b, :prefix_pages] = shared
+        pt[b, prefix_pages:prefix_pages + spages[b]] = perm[o:o + spages[b]]
+        o += spages[b]
+    kp = torch.randn((slots, hkv, psize, d), device=device).half()
+    vp = torch.randn((slots, hkv, psize, d), device=device).half()
+    return kp, vp, pt, lens.astype(np.int32), slots
+
+
+@pytest.mark.gpu
+def test_config5_shared_prefix_attention_matches_oracle(device):
+    """Qwen2-7B heads (28 query / 4 KV, GQA 7), batch 128, all sequences share a 64-page (1024-token) prefix
+    held once in the pool; suffixes 64..1024 tokens here so the oracle finishes quickly."""
+    from cacheir_amd import kernels
+
+    rng = np.random.default_rng(5)
+    kp, vp, pt, lens, _ = _shared_prefix_case(device, rng, 128, 64, 64, 1024)
+    q = rng.standard_normal((128, 28, 128)).astype(np.float16)
+    got = kernels.paged_decode_attention(to_dev(q, device), kp, vp, to_dev(pt, device), to_dev(lens, device),
+                                         check_tables=True).float().cpu().numpy()
+    ref = paged.paged_attention(q, kp.cpu().numpy(), vp.cpu().numpy(), pt, lens, 28, 4)
+    err = np.abs(got - ref) - (2e-3 + 1e-2 * np.abs(ref))
+    assert np.all(err <= 0), err.max()
+
+
+@pytest.mark.gpu
+def test_config5_full_size_aliasing_is_transparent(device):
+    """Full config-5 attention shape (batch 128, 1024-token shared prefix, suffixes 64..7168): reading the prefix
+    through aliased page-table entries gives bitwise the result of private copies of the prefix pages, and the
+    shortest/longest rows match the oracle."""
+    from cacheir_amd import kernels
+
+    rng = np.random.default_rng(7)
+    kp, vp, pt, lens, slots = _shared_prefix_case(device, rng, 128, 64, 64, 7168)
+    q = to_dev(rng.standard_normal((128, 28, 128)).astype(np.float16), device)
+    got = kernels.paged_decode_attention(q, kp, vp, to_dev(pt, device), to_dev(lens, device), check_tables=True)
+    # de-alias: every row gets its own copy of the 64 prefix pages
+    shared = pt[0, :64].copy()
+    pt2 = pt.copy()
+    extra = slots + np.arange(128 * 64, dtype=np.int32).reshape(128, 64)
+    pt2[:, :64] = extra
+    idx = torch.from_numpy(np.tile(shared, 128).astype(np.int64)).to(device)
+    kp2 = torch.cat([kp, kp.index_select(0, idx)])
+    vp2 = torch.cat([vp, vp.index_select(0, idx)])
+    got2 = kernels.paged_decode_attention(q, kp2, vp2, to_dev(pt2, device), to_dev(lens, device), check_tables=True)
+    torch.cuda.synchronize()
+    assert torch.equal(got, got2)
+    qn = q.cpu().numpy()
+    for b in (int(np.argmin(lens)), int(np.argmax(lens))):
+        n_pages = -(-int(lens[b]) // 16)
+        sl = torch.from_numpy(pt[b, :n_pages].astype(np.int64)).to(device)
+        kb, vb = kp.index_select(0, sl).cpu().numpy(), vp.index_select(0, sl).cpu().numpy()
+        ref = paged.paged_attention(qn[b:b + 1], kb, vb, np.arange(n_pages, dtype=np.int32)[None], lens[b:b + 1], 28, 4)
+        err = np.abs(got[b:b + 1].float().cpu().numpy() - ref) - (2e-3 + 1e-2 * np.abs(ref))
+        assert np.all(err <= 0), (b, err.max())
+
+
 def test_row_kernels(device):
     from cacheir_amd import kernels
 

@@ -222,3 +222,36 @@ def test_graph_capture_replays_eager(tmp_path, device):
         np.testing.assert_array_equal(plan.logits.view(3, 1, -1).cpu().numpy(), eager)
         assert plan.next_ids.cpu().tolist() == [int(np.argmax(r[-1])) for r in eager]
         _ = torch.ones(1024, device=device).sum().item()  # eager work between replays
+
+
+def test_prefix_cache_aliases_pages_with_copy_on_write(tmp_path, device):
+    """prefill_tokens(use_prefix_cache=True) reuses a cached prefix by aliasing its pages: the reusing session
+    matches a session that prefilled everything, and the prefix owner is untouched by the reuser's writes
+    (its partially filled last prefix page is copied before the reuser appends)."""
+    from cacheir_amd.runtime import HipRuntime
+
+    cfg, w, blocks, decoded = _q4_model(tmp_path, "q4_0")
+    path = write_model(tmp_path / "m", cfg, w)
+    art = compile_config(cfg, quant="q4_0", model_path=str(path))
+    owner = HipRuntime(art)
+    prefix = list(range(3, 23))          # 20 tokens: one full page + 4 tokens of the second
+    suffix = [40, 41, 42, 43, 44, 45, 46]
+    owner.prefill_tokens(prefix, remember_prefix=True)
+    reuser, full, fresh = owner.fork(), owner.fork(), owner.fork()
+    logits_r, reused = reuser.prefill_tokens(prefix + suffix, use_prefix_cache=True)
+    assert reused == tuple(prefix) and logits_r.shape[1] == len(suffix)
+    assert reuser.kv_cache.slots[0] == owner.kv_cache.slots[0]          # full page aliased
+    assert reuser.kv_cache.slots[1] != owner.kv_cache.slots[1]          # partial page copied on write
+    logits_f, _ = full.prefill_tokens(prefix + suffix)
+    close16(logits_r.cpu().numpy(), logits_f[:, len(prefix):].cpu().numpy())
+    tr, tf = int(torch.argmax(logits_r[0, -1])), int(torch.argmax(logits_f[0, -1]))
+    for _ in range(3):
+        lr, lf = reuser.run([[tr]], mode="decode"), full.run([[tf]], mode="decode")
+        close16(lr.cpu().numpy(), lf.cpu().numpy())
+        tr, tf = int(torch.argmax(lr[0, -1])), int(torch.argmax(lf[0, -1]))
+    # the owner continues exactly like a session that never shared its pages
+    fresh.prefill_tokens(prefix)
+    for tok in (7, 8):
+        assert torch.equal(owner.run([[tok]], mode="decode"), fresh.run([[tok]], mode="decode"))
+    st = owner.kv_allocator.stats()
+    assert st["shared_pages"] >= 1 and st["copied_pages"] >= 1

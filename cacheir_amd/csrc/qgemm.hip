@@ -87,8 +87,19 @@ __device__ __forceinline__ int gguf_q4_nib(const uint8_t* blk, int e) {  // elem
   return (e < 16) ? (byte & 15) : (byte >> 4);
 }
 
-__host__ __device__ size_t quant_bytes_per_lane(int fmt) { return fmt == CIR_Q4_0 ? 16 : 32; }
+// Row formats (per-row scale and zero point) reuse the tile layout of the block
+// format with the same code width: 4-bit codes sit like Q4_0 nibbles, 8-bit codes
+// like Q8_0 bytes.  Their tiled copy holds no per-block scales; after the codes come
+// fp32 scale[rows] and fp32 offset[rows] (rows padded to a multiple of 16).
+__host__ __device__ constexpr bool is_row_fmt(int fmt) { return fmt == CIR_I4_ROW || fmt == CIR_I8_ROW; }
+__host__ __device__ constexpr int layout_fmt(int fmt) {
+  return (fmt == CIR_Q4_0 || fmt == CIR_I4_ROW) ? CIR_Q4_0 : CIR_Q8_0;
+}
+__host__ __device__ size_t quant_bytes_per_lane(int fmt) { return layout_fmt(fmt) == CIR_Q4_0 ? 16 : 32; }
 __host__ __device__ size_t block_bytes(int fmt) { return fmt == CIR_Q4_0 ? 18 : 34; }
+__host__ __device__ bool valid_fmt(int fmt) {
+  return fmt == CIR_Q4_0 || fmt == CIR_Q8_0 || fmt == CIR_I4_ROW || fmt == CIR_I8_ROW;
+}
 
 // ---------------------------------------------------------------- repack ----
 __global__ void repack_kernel(const uint8_t* __restrict__ src, uint8_t* __restrict__ qdst, uint16_t* __restrict__ ddst,
@@ -141,6 +152,54 @@ __global__ void repack_kernel(const uint8_t* __restrict__ src, uint8_t* __restri
 }
 
 // ---------------------------------------------------------------- dequant ----
+// Reference per-row asymmetric packing (quantization.py:96-139) -> tiled codes + row
+// arrays.  4 bit: byte j of a row holds columns 2j (low nibble) and 2j+1 (high); the
+// code stays q (the MFMA operand is q - 8).  8 bit: one byte per column; stored as
+// q - 128 (the operand).  offset[row] = c0 - zero_point with c0 = 8 or 128, so
+// (operand + offset) * scale = (q - zp) * scale exactly.
+__global__ void repack_rows_kernel(const uint8_t* __restrict__ src, const float* __restrict__ scales,
+                                   const int32_t* __restrict__ zps, uint8_t* __restrict__ qdst,
+                                   float* __restrict__ rows_out, int fmt, int N, int K) {
+  const int KQ = K / 128;
+  const int NT = (N + 15) / 16;
+  const long total = (long)NT * KQ * 64;
+  const long id = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= total) return;
+  const int lane = (int)(id & 63);
+  const long tile = id >> 6;
+  const int Q = (int)(tile % KQ);
+  const int nt = (int)(tile / KQ);
+  const int r = lane & 15, g = lane >> 4;
+  const int n = nt * 16 + r;
+  if (fmt == CIR_I4_ROW) {
+    const size_t row_bytes = (size_t)(K + 1) / 2;
+    uint32_t* out = reinterpret_cast<uint32_t*>(qdst + ((size_t)tile * 64 + lane) * 16);
+    for (int j = 0; j < 4; ++j) {
+      uint32_t w = 0;
+      if (n < N) {
+        for (int nu = 0; nu < 8; ++nu) {
+          const int col = 128 * Q + 32 * j + 8 * g + q4_elem_of_nibble(nu);
+          const uint8_t byte = src[(size_t)n * row_bytes + col / 2];
+          w |= (uint32_t)((col & 1) ? (byte >> 4) : (byte & 15)) << (4 * nu);
+        }
+      }
+      out[j] = w;
+    }
+  } else {
+    uint8_t* out = qdst + ((size_t)tile * 64 + lane) * 32;
+    for (int j = 0; j < 4; ++j)
+      for (int beta = 0; beta < 8; ++beta) {
+        const int col = 128 * Q + 32 * j + 8 * g + q8_elem_of_byte(beta);
+        out[8 * j + beta] = n < N ? (uint8_t)(src[(size_t)n * K + col] - 128u) : (uint8_t)0;
+      }
+  }
+  if (Q == 0 && g == 0) {
+    const int c0 = fmt == CIR_I4_ROW ? 8 : 128;
+    rows_out[(size_t)nt * 16 + r] = n < N ? scales[n] : 0.f;
+    rows_out[(size_t)NT * 16 + (size_t)nt * 16 + r] = n < N ? (float)(c0 - zps[n]) : 0.f;
+  }
+}
+
 __global__ void dequant_gguf_kernel(const uint8_t* __restrict__ src, float* __restrict__ out, int fmt, int N, int K) {
   const long nblk = (long)N * (K / 32);
   const long b = (long)blockIdx.x * blockDim.x + threadIdx.x;
@@ -156,7 +215,7 @@ __global__ void dequant_gguf_kernel(const uint8_t* __restrict__ src, float* __re
   }
 }
 
-__global__ void dequant_tiled_kernel(const uint8_t* __restrict__ q, const uint16_t* __restrict__ dsc,
+__global__ void dequant_tiled_kernel(const uint8_t* __restrict__ q, const void* __restrict__ scales_any,
                                      float* __restrict__ out, int fmt, int N, int K) {
   // One thread per (tile, lane): 32 values (4 k-steps x 8).
   const int KQ = K / 128;
@@ -170,15 +229,25 @@ __global__ void dequant_tiled_kernel(const uint8_t* __restrict__ q, const uint16
   const int r = lane & 15, g = lane >> 4;
   const int n = nt * 16 + r;
   if (n >= N) return;
+  const uint16_t* dsc = static_cast<const uint16_t*>(scales_any);
+  const float* rsc = static_cast<const float*>(scales_any);
   for (int j = 0; j < 4; ++j) {
-    const float d = static_cast<float>(__builtin_bit_cast(f16, dsc[((size_t)tile * 16 + r) * 4 + j]));
+    // block formats: value = operand * d; row formats: (operand + offset) * scale
+    float d, off = 0.f;
+    if (is_row_fmt(fmt)) {
+      d = rsc[n];
+      off = rsc[(size_t)NT * 16 + n];
+    } else {
+      d = static_cast<float>(__builtin_bit_cast(f16, dsc[((size_t)tile * 16 + r) * 4 + j]));
+    }
     float* o = out + (size_t)n * K + 128 * Q + 32 * j + 8 * g;
-    if (fmt == CIR_Q4_0) {
+    if (layout_fmt(fmt) == CIR_Q4_0) {
       const uint32_t w = reinterpret_cast<const uint32_t*>(q + ((size_t)tile * 64 + lane) * 16)[j];
-      for (int nu = 0; nu < 8; ++nu) o[q4_elem_of_nibble(nu)] = (float)((int)((w >> (4 * nu)) & 15) - 8) * d;
+      for (int nu = 0; nu < 8; ++nu)
+        o[q4_elem_of_nibble(nu)] = ((float)((int)((w >> (4 * nu)) & 15) - 8) + off) * d;
     } else {
       const uint8_t* bytes = q + ((size_t)tile * 64 + lane) * 32 + 8 * j;
-      for (int beta = 0; beta < 8; ++beta) o[q8_elem_of_byte(beta)] = (float)(int8_t)bytes[beta] * d;
+      for (int beta = 0; beta < 8; ++beta) o[q8_elem_of_byte(beta)] = ((float)(int8_t)bytes[beta] + off) * d;
     }
   }
 }
@@ -188,7 +257,7 @@ __global__ void dequant_tiled_kernel(const uint8_t* __restrict__ q, const uint16
 // scales) and the MT activation tiles as MFMA A operands.
 template <int FMT, int NT, int MT>
 struct Stage {
-  static constexpr int LB = (FMT == CIR_Q4_0) ? 1 : 2;  // 16-byte loads per lane per weight tile
+  static constexpr int LB = (layout_fmt(FMT) == CIR_Q4_0) ? 1 : 2;  // 16-byte loads per lane per weight tile
   uint4 w[NT][LB];
   uint2 d[NT];
   f16x8 x[MT][4];
@@ -206,26 +275,45 @@ __device__ __forceinline__ void compute_stage(const Stage<FMT, NT, MT>& st, f32x
 #pragma unroll
     for (int b = 0; b < NT; ++b) {
       f16x8 wb;
-      if constexpr (FMT == CIR_Q4_0) {
+      if constexpr (layout_fmt(FMT) == CIR_Q4_0) {
         const uint4 v = st.w[b][0];
         wb = dq_q4((j == 0) ? v.x : (j == 1) ? v.y : (j == 2) ? v.z : v.w);
       } else {
         const uint4 v = st.w[b][j >> 1];
         wb = dq_q8((j & 1) ? v.z : v.x, (j & 1) ? v.w : v.y);
       }
-      const uint32_t dw = (j < 2) ? st.d[b].x : st.d[b].y;
-      dj[b] = static_cast<float>(__builtin_bit_cast(f16, (uint16_t)((j & 1) ? (dw >> 16) : (dw & 0xFFFFu))));
+      if constexpr (is_row_fmt(FMT)) {
+        // one scale per row: integers accumulate over all k in the MFMA itself
 #pragma unroll
-      for (int a = 0; a < MT; ++a)
-        c[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(st.x[a][j], wb, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+        for (int a = 0; a < MT; ++a) acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(st.x[a][j], wb, acc[a][b], 0, 0, 0);
+      } else {
+        const uint32_t dw = (j < 2) ? st.d[b].x : st.d[b].y;
+        dj[b] = static_cast<float>(__builtin_bit_cast(f16, (uint16_t)((j & 1) ? (dw >> 16) : (dw & 0xFFFFu))));
+#pragma unroll
+        for (int a = 0; a < MT; ++a)
+          c[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(st.x[a][j], wb, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+      }
     }
+    if constexpr (!is_row_fmt(FMT)) {
 #pragma unroll
-    for (int b = 0; b < NT; ++b)
+      for (int b = 0; b < NT; ++b)
 #pragma unroll
-      for (int a = 0; a < MT; ++a)
+        for (int a = 0; a < MT; ++a)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) acc[a][b][r] = fmaf(dj[b], c[a][b][r], acc[a][b][r]);
+          for (int r = 0; r < 4; ++r) acc[a][b][r] = fmaf(dj[b], c[a][b][r], acc[a][b][r]);
+    }
   }
+}
+
+// Row sums of the activation quad (row formats): sx[a] += x[16a + 4*lg + r][quad] . 1,
+// by MFMA against an all-ones B operand, so the C layout matches the accumulators'.
+template <int MT>
+__device__ __forceinline__ void row_sums(const f16x8 (&x)[MT][4], f32x4 (&sx)[MT]) {
+  const f16x8 ones = {1, 1, 1, 1, 1, 1, 1, 1};
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int a = 0; a < MT; ++a) sx[a] = __builtin_amdgcn_mfma_f32_16x16x32_f16(x[a][j], ones, sx[a], 0, 0, 0);
 }
 
 // Dense fp32: one wavefront per output row n, lanes over k; all m rows.
@@ -323,7 +411,7 @@ __global__ __launch_bounds__(256) void qgemm_xs_kernel(const f16* __restrict__ x
       const uint4* src = wbase[b] + (size_t)Q * (64 * LB);
 #pragma unroll
       for (int c = 0; c < LB; ++c) ws[slot_w].w[b][c] = src[c];
-      ws[slot_w].d[b] = dbase[b][(size_t)Q * 16];
+      if constexpr (!is_row_fmt(FMT)) ws[slot_w].d[b] = dbase[b][(size_t)Q * 16];
     }
   };
   auto put_x = [&](int slot_x, const XsChunk<MT>& ch) __attribute__((always_inline)) {
@@ -333,10 +421,13 @@ __global__ __launch_bounds__(256) void qgemm_xs_kernel(const f16* __restrict__ x
   auto barrier = [] { __syncthreads(); };
 
   f32x4 acc[MT][NT];
+  f32x4 sx[MT];  // row formats: sums of this split's activations, per output row
 #pragma unroll
-  for (int a = 0; a < MT; ++a)
+  for (int a = 0; a < MT; ++a) {
+    sx[a] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int b = 0; b < NT; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
 
   auto compute = [&](const WS& st, int slot_x) __attribute__((always_inline)) {
     Stage<FMT, NT, MT> sg;  // reuse compute_stage: fragments from LDS, weights from the ring
@@ -349,9 +440,10 @@ __global__ __launch_bounds__(256) void qgemm_xs_kernel(const f16* __restrict__ x
     for (int b = 0; b < NT; ++b) {
 #pragma unroll
       for (int c = 0; c < LB; ++c) sg.w[b][c] = st.w[b][c];
-      sg.d[b] = st.d[b];
+      if constexpr (!is_row_fmt(FMT)) sg.d[b] = st.d[b];
     }
     compute_stage(sg, acc);
+    if constexpr (is_row_fmt(FMT)) row_sums(sg.x, sx);
   };
 
   // Ring slots are template arguments (std::integer_sequence), so every ring access
@@ -383,6 +475,21 @@ __global__ __launch_bounds__(256) void qgemm_xs_kernel(const f16* __restrict__ x
     }
   });
 
+  if constexpr (is_row_fmt(FMT)) {
+    // w = (c - zp) * s with c the stored code: acc holds sum x*c over this split, so
+    // the split's share of y is s * (acc + (c0 - zp) * sum x), c0 - zp = offset[row].
+    const float* rscale = reinterpret_cast<const float*>(wd);
+    const float* roff = rscale + (size_t)NTILES * 16;
+#pragma unroll
+    for (int b = 0; b < NT; ++b) {
+      const int n = min(nt0 + b, NTILES - 1) * 16 + li;
+      const float sc = rscale[n], of = roff[n];
+#pragma unroll
+      for (int a = 0; a < MT; ++a)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[a][b][r] = sc * fmaf(of, sx[a][r], acc[a][b][r]);
+    }
+  }
   if constexpr (EPI == 1) {
     const int inter = N / 2;
     const int col = (nt0 >> 1) * 16 + li;
@@ -458,9 +565,25 @@ void dispatch_qgemm(const f16* x, int ldx, const uint8_t* wq, const uint16_t* wd
 using namespace cir;
 
 extern "C" size_t cir_qweight_tiled_bytes(int fmt, int n, int k) {
-  if ((fmt != CIR_Q4_0 && fmt != CIR_Q8_0) || n <= 0 || k <= 0 || k % 128) return 0;
+  if (!valid_fmt(fmt) || n <= 0 || k <= 0 || k % 128) return 0;
   const size_t tiles = (size_t)((n + 15) / 16) * (k / 128);
+  if (is_row_fmt(fmt)) return tiles * 64 * quant_bytes_per_lane(fmt) + (size_t)((n + 15) / 16) * 16 * 2 * sizeof(float);
   return tiles * (64 * quant_bytes_per_lane(fmt) + 16 * 4 * sizeof(uint16_t));
+}
+
+extern "C" int cir_qweight_repack_rows(const void* packed, const float* scales, const int32_t* zero_points, void* tiled,
+                                       int fmt, int n, int k, void* stream) {
+  CIR_CHECK_ARG(is_row_fmt(fmt), "repack_rows: fmt must be CIR_I4_ROW or CIR_I8_ROW (got %d)", fmt);
+  CIR_CHECK_ARG(n >= 0 && k >= 0 && k % 128 == 0, "repack_rows: k (%d) must be a multiple of 128", k);
+  if (n == 0 || k == 0) return 0;
+  CIR_CHECK_ARG(packed && scales && zero_points && tiled, "repack_rows: null pointer");
+  const size_t tiles = (size_t)((n + 15) / 16) * (k / 128);
+  uint8_t* q = static_cast<uint8_t*>(tiled);
+  float* rows = reinterpret_cast<float*>(q + tiles * 64 * quant_bytes_per_lane(fmt));
+  const long threads = (long)tiles * 64;
+  repack_rows_kernel<<<(unsigned)((threads + 255) / 256), 256, 0, as_stream(stream)>>>(
+      static_cast<const uint8_t*>(packed), scales, zero_points, q, rows, fmt, n, k);
+  return launch_status();
 }
 
 extern "C" int cir_qweight_repack(const void* gguf_blocks, void* tiled, int fmt, int n, int k, void* stream) {
@@ -478,7 +601,8 @@ extern "C" int cir_qweight_repack(const void* gguf_blocks, void* tiled, int fmt,
 }
 
 extern "C" int cir_dequant(const void* weights, int tiled, int fmt, float* out, int n, int k, void* stream) {
-  CIR_CHECK_ARG(fmt == CIR_Q4_0 || fmt == CIR_Q8_0, "dequant: fmt must be CIR_Q4_0 or CIR_Q8_0 (got %d)", fmt);
+  CIR_CHECK_ARG(valid_fmt(fmt), "dequant: unknown weight format %d", fmt);
+  CIR_CHECK_ARG(tiled || !is_row_fmt(fmt), "dequant: row formats are read from their tiled copy (tiled = 1)");
   CIR_CHECK_ARG(n >= 0 && k >= 0 && k % 32 == 0, "dequant: k (%d) must be a multiple of 32", k);
   if (n == 0 || k == 0) return 0;
   CIR_CHECK_ARG(weights && out, "dequant: null pointer");
@@ -491,7 +615,7 @@ extern "C" int cir_dequant(const void* weights, int tiled, int fmt, float* out, 
     CIR_CHECK_ARG(k % 128 == 0, "dequant: tiled weights need k %% 128 == 0");
     const size_t tiles = (size_t)((n + 15) / 16) * (k / 128);
     const uint8_t* q = static_cast<const uint8_t*>(weights);
-    const uint16_t* d = reinterpret_cast<const uint16_t*>(q + tiles * 64 * quant_bytes_per_lane(fmt));
+    const void* d = q + tiles * 64 * quant_bytes_per_lane(fmt);
     const long threads = (long)tiles * 64;
     dequant_tiled_kernel<<<(unsigned)((threads + 255) / 256), 256, 0, s>>>(q, d, out, fmt, n, k);
   }
@@ -510,7 +634,7 @@ extern "C" size_t cir_qgemm_workspace_bytes(int m, int n, int splits) {
 
 extern "C" int cir_qgemm(const void* x, int ldx, const void* w_tiled, int fmt, float* y_partial, int m, int n, int k,
                          int splits, void* stream) {
-  CIR_CHECK_ARG(fmt == CIR_Q4_0 || fmt == CIR_Q8_0, "qgemm: fmt must be CIR_Q4_0 or CIR_Q8_0 (got %d)", fmt);
+  CIR_CHECK_ARG(valid_fmt(fmt), "qgemm: unknown weight format %d", fmt);
   CIR_CHECK_ARG(m >= 0 && n >= 0 && k >= 0, "qgemm: negative size");
   if (m == 0 || n == 0) return 0;
   CIR_CHECK_ARG(k > 0 && k % 128 == 0, "qgemm: k (%d) must be a positive multiple of 128", k);
@@ -525,15 +649,19 @@ extern "C" int cir_qgemm(const void* x, int ldx, const void* w_tiled, int fmt, f
   hipStream_t s = as_stream(stream);
   if (fmt == CIR_Q4_0) {
     dispatch_qgemm<CIR_Q4_0>(xh, ldx, q, d, y_partial, m, n, k, splits, s);
-  } else {
+  } else if (fmt == CIR_Q8_0) {
     dispatch_qgemm<CIR_Q8_0>(xh, ldx, q, d, y_partial, m, n, k, splits, s);
+  } else if (fmt == CIR_I4_ROW) {
+    dispatch_qgemm<CIR_I4_ROW>(xh, ldx, q, d, y_partial, m, n, k, splits, s);
+  } else {
+    dispatch_qgemm<CIR_I8_ROW>(xh, ldx, q, d, y_partial, m, n, k, splits, s);
   }
   return launch_status();
 }
 
 extern "C" int cir_qgemm_swiglu(const void* x, int ldx, const void* w_tiled, int fmt, void* out, int odt, int m,
                                 int inter, int k, void* stream) {
-  CIR_CHECK_ARG(fmt == CIR_Q4_0 || fmt == CIR_Q8_0, "qgemm_swiglu: fmt must be CIR_Q4_0 or CIR_Q8_0 (got %d)", fmt);
+  CIR_CHECK_ARG(valid_fmt(fmt), "qgemm_swiglu: unknown weight format %d", fmt);
   CIR_CHECK_ARG(odt == CIR_F16 || odt == CIR_F32, "qgemm_swiglu: out dtype must be CIR_F16 or CIR_F32");
   CIR_CHECK_ARG(m >= 0 && inter >= 0 && k >= 0, "qgemm_swiglu: negative size");
   if (m == 0 || inter == 0) return 0;
@@ -558,7 +686,9 @@ extern "C" int cir_qgemm_swiglu(const void* x, int ldx, const void* w_tiled, int
     }
   };
   if (fmt == CIR_Q4_0) go.template operator()<CIR_Q4_0>();
-  else go.template operator()<CIR_Q8_0>();
+  else if (fmt == CIR_Q8_0) go.template operator()<CIR_Q8_0>();
+  else if (fmt == CIR_I4_ROW) go.template operator()<CIR_I4_ROW>();
+  else go.template operator()<CIR_I8_ROW>();
   return launch_status();
 }
 

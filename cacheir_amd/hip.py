@@ -22,6 +22,8 @@ CIR_F32 = 0
 CIR_F16 = 1
 CIR_Q4_0 = 2
 CIR_Q8_0 = 8
+CIR_I4_ROW = 64  # the reference's per-row asymmetric int4 packing
+CIR_I8_ROW = 65  # ... and int8
 
 _c_int, _c_size, _c_float, _vp = ctypes.c_int, ctypes.c_size_t, ctypes.c_float, ctypes.c_void_p
 
@@ -38,6 +40,7 @@ _SIGNATURES = {
                                              _c_int, _c_int, _c_int, _c_float, _c_int, _vp]),
     "cir_qweight_tiled_bytes": (_c_size, [_c_int, _c_int, _c_int]),
     "cir_qweight_repack": (_c_int, [_vp, _vp, _c_int, _c_int, _c_int, _vp]),
+    "cir_qweight_repack_rows": (_c_int, [_vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp]),
     "cir_dequant": (_c_int, [_vp, _c_int, _c_int, _vp, _c_int, _c_int, _vp]),
     "cir_qgemm_splits": (_c_int, [_c_int, _c_int, _c_int]),
     "cir_qgemm_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int]),

@@ -130,7 +130,7 @@ def paged_prefill_attention(q, k_pool, v_pool, page_table, seq_lens, q_len: int,
 # -------------------------------------------------------------- block weights --
 @dataclass
 class QWeight:
-    """A Q4_0/Q8_0 weight ``W[n, k]`` kept on the device in the tiled layout."""
+    """A Q4_0/Q8_0 (or per-row asymmetric int4/int8) weight ``W[n, k]`` kept on the device in the tiled layout."""
 
     tiled: torch.Tensor  # uint8
     fmt: int
@@ -144,6 +144,26 @@ class QWeight:
     @property
     def nbytes(self) -> int:
         return self.tiled.numel()
+
+    @classmethod
+    def from_rows(cls, packed: torch.Tensor, scales: torch.Tensor, zero_points: torch.Tensor, bits: int, n: int,
+                  k: int) -> "QWeight":
+        """Repack the reference's per-row asymmetric packing (uint8 codes ``[n, ceil(k/2)]`` for 4 bit or
+        ``[n, k]`` for 8 bit, fp32 scales ``[n]``, int32 zero points ``[n]``, on the GPU) into the tiled layout."""
+        for t, name in ((packed, "packed"), (scales, "scales"), (zero_points, "zero_points")):
+            _cuda(t, name)
+        _req(bits in (4, 8), f"bits must be 4 or 8 (got {bits})")
+        _req(k % 128 == 0, f"k={k} must be a multiple of 128 for the tiled GEMM")
+        row_bytes = (k + 1) // 2 if bits == 4 else k
+        _req(packed.dtype == torch.uint8 and packed.numel() == n * row_bytes, "packed codes must be uint8 [n, row_bytes]")
+        _req(scales.dtype == torch.float32 and scales.numel() == n, "scales must be float32 [n]", TypeError)
+        _req(zero_points.dtype == torch.int32 and zero_points.numel() == n, "zero_points must be int32 [n]", TypeError)
+        fmt = hip.CIR_I4_ROW if bits == 4 else hip.CIR_I8_ROW
+        size = hip.size_call("cir_qweight_tiled_bytes", fmt, n, k)
+        tiled = torch.empty(size, dtype=torch.uint8, device=packed.device)
+        hip.call("cir_qweight_repack_rows", packed.data_ptr(), scales.data_ptr(), zero_points.data_ptr(),
+                 tiled.data_ptr(), fmt, n, k, hip.stream_handle())
+        return cls(tiled, fmt, n, k)
 
     @classmethod
     def from_blocks(cls, blocks: torch.Tensor, fmt: int, n: int, k: int) -> "QWeight":

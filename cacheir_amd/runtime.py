@@ -40,7 +40,7 @@ from cacheir_amd import hip, kernels
 from cacheir_amd.artifact import CompileArtifact
 from cacheir_amd.ir import Graph, Node
 from cacheir_amd.kv import HipKVPageAllocator, HipPagedKVCache
-from cacheir_amd.weights import GGUFSource, HipWeightStore, NpzDir, SyntheticQuant
+from cacheir_amd.weights import GGUFSource, HipWeightStore, NpzDir, SyntheticQuant, row_bits
 
 _QKV_OPS = {"fused_rmsnorm_qkv_rope", "quantized_fused_rmsnorm_qkv_rope"}
 _SWIGLU_OPS = {"fused_swiglu", "quantized_fused_swiglu"}
@@ -439,7 +439,8 @@ class HipRuntime:
         quant = (self.artifact.quant or "").lower() or None
         if weights is None:
             source = source if source is not None else self._open_source()
-            blocked = quant in {"q4_0", "q8_0"} or isinstance(source, (GGUFSource, SyntheticQuant))
+            blocked = (quant in {"q4_0", "q8_0"} or row_bits(quant) is not None
+                       or isinstance(source, (GGUFSource, SyntheticQuant)))
             self.dtype = self._select_dtype(dtype, blocked)
             dense_dtype = torch.float16 if self.dtype == torch.float16 else torch.float32
             weights = HipWeightStore(source, graph.weights, device=self.device, dense_dtype=dense_dtype, quant=quant)

@@ -118,6 +118,38 @@ class GGUFFile:
 
 
 # ---------------------------------------------------------- host quantizers ----
+def row_bits(quant: str | None) -> int | None:
+    """Bit width of the reference's per-row asymmetric packing for a ``--quant`` name
+    (``quantization.py:63-71``: int4 / awq / gptq -> 4, int8 / 8bit -> 8), else None."""
+    name = (quant or "").lower()
+    if not name or name in ("q4_0", "q8_0"):
+        return None
+    if "int4" in name or "awq" in name or "gptq" in name:
+        return 4
+    if "int8" in name or "8bit" in name:
+        return 8
+    return None
+
+
+def pack_rows(w: np.ndarray, bits: int) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """The reference's per-row asymmetric packing of ``W[out, in]`` (``quantization.py:96-139``):
+    scale = max((max - min) / qmax, 1e-8), zero_point = round(-min / scale), q = clip(round(w / scale + zp),
+    0, qmax); 4-bit codes two per byte (even column low nibble).  Returns (packed uint8, scales fp32,
+    zero_points int32), the ``PackedQuantizedTensor`` fields."""
+    a = np.asarray(w, dtype=np.float32)
+    qmax = (1 << bits) - 1
+    mins, maxs = a.min(axis=1), a.max(axis=1)
+    scales = np.maximum((maxs - mins) / np.float32(qmax), np.float32(1.0e-8)).astype(np.float32)
+    zps = np.round(np.float32(0) - mins / scales).astype(np.int32)
+    q = np.round(a / scales[:, None] + zps[:, None]).clip(0, qmax).astype(np.uint8)
+    if bits == 4:
+        rows, cols = q.shape
+        padded = np.zeros((rows, cols + (cols % 2)), dtype=np.uint8)
+        padded[:, :cols] = q & 0x0F
+        q = (padded[:, 0::2] | (padded[:, 1::2] << 4)).astype(np.uint8)
+    return np.ascontiguousarray(q), np.ascontiguousarray(scales), np.ascontiguousarray(zps)
+
+
 def quantize_q4_0(w: np.ndarray) -> np.ndarray:
     """Dense ``[n, k]`` -> GGUF Q4_0 bytes: per block d = m / -8 where m is the value of
     largest magnitude, q = min(15, floor(x/d + 8.5)) (the ggml reference quantizer)."""
@@ -251,14 +283,38 @@ class HipWeightStore:
         return self._dense[key]
 
     def is_blocked(self, names: tuple[str, ...]) -> bool:
+        """True when `names` run on the quantized MFMA GEMM (GGUF blocks or the reference's row packing)."""
         keys = [self.specs[n].key for n in names]
-        if self.quant in _FMT_OF:
+        if self.quant in _FMT_OF or row_bits(self.quant):
             return True
         return all(self.source.has_blocks(k) for k in keys)
+
+    def _row_packed(self, names: tuple[str, ...], interleave: bool = False) -> "kernels.QWeight":
+        """Per-row asymmetric int4/int8 packing of the concatenated rows of `names` (each row keeps its own scale and
+        zero point, exactly as the reference packs each matrix); `interleave` pairs 16-row tiles of two weights."""
+        bits = row_bits(self.quant)
+        parts = [pack_rows(np.asarray(self.source.dense(self.specs[n].key), dtype=np.float32), bits) for n in names]
+        k = int(self.specs[names[0]].tensor_type.shape[1])
+        if interleave:
+            rows = parts[0][0].shape[0]
+            def il(a, b):
+                return np.stack([a.reshape(rows // 16, 16, -1), b.reshape(rows // 16, 16, -1)], axis=1).reshape(2 * rows, -1)
+            packed = il(parts[0][0], parts[1][0])
+            scales = il(parts[0][1][:, None], parts[1][1][:, None]).reshape(-1)
+            zps = il(parts[0][2][:, None], parts[1][2][:, None]).reshape(-1)
+        else:
+            packed = np.concatenate([p[0] for p in parts])
+            scales = np.concatenate([p[1] for p in parts])
+            zps = np.concatenate([p[2] for p in parts])
+        dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(self.device)
+        return kernels.QWeight.from_rows(dev(packed), dev(scales), dev(zps), bits, packed.shape[0], k)
 
     # -- matmul weights: one QWeight (or dense [n, k] tensor) for the concatenation of `names` --
     def matmul_weight(self, names: tuple[str, ...]):
         if names in self._packed:
+            return self._packed[names]
+        if row_bits(self.quant):
+            self._packed[names] = self._row_packed(names)
             return self._packed[names]
         if self.is_blocked(names):
             parts, fmt, k = [], None, None
@@ -281,6 +337,8 @@ class HipWeightStore:
         """Gate and up block weights as one tiled weight with their 16-row tiles interleaved (gate c, up c, ...),
         the layout ``cir_qgemm_swiglu`` reads."""
         key = (gate, up, "swiglu")
+        if key not in self._packed and row_bits(self.quant):
+            self._packed[key] = self._row_packed((gate, up), interleave=True)
         if key not in self._packed:
             (gb, gf, rows, k), (ub, uf, rows_u, ku) = self._blocks(gate), self._blocks(up)
             if gf != uf or k != ku or rows != rows_u:

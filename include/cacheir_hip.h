@@ -16,7 +16,8 @@
  *     host threads on different streams.
  *
  * Dtype codes: CIR_F32 = 0, CIR_F16 = 1.  Weight formats use GGML type ids:
- * CIR_Q4_0 = 2, CIR_Q8_0 = 8.
+ * CIR_Q4_0 = 2, CIR_Q8_0 = 8; the reference's own per-row asymmetric int4 / int8
+ * packing is CIR_I4_ROW = 64 / CIR_I8_ROW = 65.
  */
 #ifndef CACHEIR_HIP_H
 #define CACHEIR_HIP_H
@@ -32,6 +33,11 @@ extern "C" {
 #define CIR_F16 1
 #define CIR_Q4_0 2
 #define CIR_Q8_0 8
+/* Per-row asymmetric formats of the reference (cacheir/quantization.py:96-139,
+ * PackedQuantizedTensor with axis 1): w = (q - zero_point[row]) * scale[row], q in
+ * [0, 15] (4 bit) or [0, 255] (8 bit). */
+#define CIR_I4_ROW 64
+#define CIR_I8_ROW 65
 
 /* Library identity and diagnostics. */
 const char* cir_version(void);
@@ -93,6 +99,18 @@ int cir_paged_prefill_attention(const void* q, const void* k_pool, const void* v
  * same (q - 8) * d (Q4_0) or q * d (Q8_0) as the GGUF blocks. */
 size_t cir_qweight_tiled_bytes(int fmt, int n, int k);
 int cir_qweight_repack(const void* gguf_blocks, void* tiled, int fmt, int n, int k, void* stream);
+
+/* The reference's own per-row asymmetric packing (cacheir/quantization.py:96-139,
+ * PackedQuantizedTensor produced for --quant int4 / int4_awq / gptq / int8 and
+ * consumed by cacheir/runtime/cuda.py:77-105,932-954) -> the tiled copy cir_qgemm
+ * reads (fmt CIR_I4_ROW or CIR_I8_ROW, cir_qweight_tiled_bytes bytes).
+ * packed: uint8 [n][ceil(k/2)] (4 bit: column 2j in the low nibble of byte j, 2j+1 in
+ * the high nibble) or [n][k] (8 bit); scales fp32 [n]; zero_points int32 [n].
+ * cir_dequant(tiled = 1) then gives exactly (q - zero_point) * scale in fp32, and
+ * cir_qgemm multiplies the exact integer codes, applying scale and zero point per row
+ * after the k-sum. */
+int cir_qweight_repack_rows(const void* packed, const float* scales, const int32_t* zero_points, void* tiled,
+                            int fmt, int n, int k, void* stream);
 
 /* Bit-exact dequantization to fp32 [n, k] from GGUF blocks (tiled = 0) or from the
  * tiled copy (tiled = 1).  Replaces gguf.py:273-310 for device-resident weights. */

@@ -179,3 +179,22 @@ def test_prefix_cache_holds_and_releases_pages():
     pc.clear()
     s2.clear()
     assert a.stats()["resident_pages"] == 0
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("cols", [256, 257])
+def test_row_packer_matches_reference_restatement(bits, cols):
+    """cacheir_amd.weights.pack_rows (product) == oracle.quant.asymmetric_pack (the restatement pinned to the
+    reference's own case), bit for bit, incl. an odd column count and rows of one sign."""
+    from cacheir_amd.weights import pack_rows, row_bits
+
+    rng = np.random.default_rng(bits * 1000 + cols)
+    w = rng.standard_normal((24, cols)).astype(np.float32)
+    w[3] = np.abs(w[3]) + 0.5     # all positive: zero point below 0
+    w[5] = -np.abs(w[5]) - 0.5    # all negative: zero point above qmax
+    w[7] = 0.25                   # constant row: scale floor 1e-8
+    packed, scales, zps = pack_rows(w, bits)
+    ref = quant.asymmetric_pack(w, bits)
+    assert np.array_equal(packed, ref["packed_values"])
+    assert np.array_equal(scales, ref["scales"]) and np.array_equal(zps, ref["zero_points"])
+    assert row_bits("int4_awq") == 4 and row_bits("gptq") == 4 and row_bits("int8") == 8 and row_bits("q4_0") is None

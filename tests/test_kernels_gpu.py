@@ -380,6 +380,32 @@ def test_config5_full_size_aliasing_is_transparent(device):
         assert np.all(err <= 0), (b, err.max())
 
 
+@pytest.mark.gpu
+@pytest.mark.parametrize("bits", [4, 8])
+def test_row_packed_dequant_bit_exact_and_gemm(device, bits):
+    """The reference's per-row asymmetric int4/int8 packing through cir_qweight_repack_rows: dequant equals
+    quantization.py's (q - zp) * scale bit for bit; the GEMM is within the fp16 bound of fp64 on those weights."""
+    from cacheir_amd import kernels
+
+    rng = np.random.default_rng(bits)
+    n, k = 200, 384  # n not a multiple of 16
+    w = rng.standard_normal((n, k)).astype(np.float32) * 0.05
+    w[0] = np.abs(w[0]) + 0.01
+    pk = quant.asymmetric_pack(w, bits)
+    qw = kernels.QWeight.from_rows(to_dev(pk["packed_values"], device), to_dev(pk["scales"], device),
+                                   to_dev(pk["zero_points"], device), bits, n, k)
+    deq = quant.asymmetric_dequant(pk)
+    got = kernels.dequant_tiled(qw).cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), deq.astype(np.float32).view(np.uint32))
+    for m in (1, 8, 32):
+        x = rng.standard_normal((m, k)).astype(np.float16)
+        for splits in (1, 3):
+            y = kernels.qgemm_partial(to_dev(x, device), qw, splits=splits).sum(0).double().cpu().numpy()
+            ref = x.astype(np.float64) @ deq.astype(np.float64).T
+            err = np.abs(y - ref) - (2e-3 + 1e-2 * np.abs(ref))
+            assert np.all(err <= 0), (m, splits, err.max())
+
+
 def test_row_kernels(device):
     from cacheir_amd import kernels
 

@@ -36,13 +36,15 @@ namespace cir {
 namespace {
 
 // 8 wavefronts of 32-token steps measured best on MI355X at config 4 (batch 32,
-// 2048 tokens): 53.7 us = 5.0 TB/s against 61 us for 64-token steps, 56 us for 16
-// wavefronts of 16 tokens and 55 us for a double-buffered 16-token pipeline.  A pure
-// streaming read peaks at ~6.2 TB/s on this part.
+// 2048 tokens), against 64-token steps, 16 wavefronts of 16 tokens and a
+// double-buffered pipeline.  A pure streaming read peaks at ~6.2 TB/s on this part;
+// a loads-only copy of this kernel's access pattern (same grid, pages and per-lane
+// addresses) reaches ~5.5 TB/s, and the kernel about 88% of that.
 constexpr int kTiles = 2;             // 16-token MFMA tiles per wavefront step
 constexpr int kBlock = 16 * kTiles;   // tokens per wavefront step
 constexpr int kWaves = 8;             // wavefronts per workgroup (fp16 path)
 constexpr int kChunk = 128;  // tokens per partial in the generic path
+constexpr int kPtCache = 512;  // page-table entries a workgroup keeps in LDS (2 KiB)
 constexpr int kMinSplitTokens = 256;
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -85,9 +87,13 @@ __global__ __launch_bounds__(64 * kWaves) void attn_f16_d128(
   __shared__ float sm_l[kWaves][16];
   __shared__ float sm_o[kWaves][G][D];
   __shared__ __align__(16) f16 sm_q[G][D];
+  __shared__ int sm_pt[kPtCache];
 
   const int split = blockIdx.x, kvh = blockIdx.y, row = blockIdx.z;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  // readfirstlane: the wavefront index is uniform, so block indices and page-table
+  // lookups stay scalar (s_load, their own counter) instead of vector loads that
+  // would retire in order behind the K/V loads in flight.
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int li = lane & 15;  // score column (token in tile) / Q row (head in group)
   const int lg = lane >> 4;  // k-group of the MFMA operands; token group for P V
   const int L = visible_len(lens, row, q_len, max_pages * P);
@@ -97,6 +103,69 @@ __global__ __launch_bounds__(64 * kWaves) void attn_f16_d128(
   const int b = row / q_len;
   const int32_t* ptrow = pt + (size_t)b * max_pages;
 
+  // One block of K/V operands (kTiles 16-token tiles) for one wavefront.
+  struct Blk {
+    f16x8 k[kTiles][4], v[kTiles][4];
+  };
+  // Issue every K load, then every V load, of block `blk` (K first: the scores need
+  // only K, so they start while V is still arriving).  Tiles past the end re-read
+  // the block's first tile (masked in the scores).
+  // This split's page-table entries, cached in LDS when they fit (filled before the
+  // first workgroup barrier; until then lookups read the table directly).
+  const int pg0 = (b0 * kBlock) / P;
+  const int pg1 = min(max_pages, (b1 * kBlock + P - 1) / P);
+  const bool pt_cached = pg1 - pg0 <= kPtCache;
+  bool pt_ready = false;
+  auto page_of = [&](int t) __attribute__((always_inline)) {
+    const int pi = t / P;
+    return (pt_ready && pt_cached) ? __builtin_amdgcn_readfirstlane(sm_pt[pi - pg0]) : ptrow[pi];
+  };
+  auto page_bases = [&](size_t (&base)[kTiles], int blk) __attribute__((always_inline)) {
+    const int tb = blk * kBlock;
+#pragma unroll
+    for (int j = 0; j < kTiles; ++j) {
+      const int tj = tb + 16 * j;
+      const int tv = tj < L ? tj : tb;
+      const int page = page_of(tv);
+      base[j] = (((size_t)page * Hkv + kvh) * P + (tv % P)) * D;
+    }
+  };
+  auto load_k = [&](Blk& o, int blk) __attribute__((always_inline)) {
+    size_t base[kTiles];
+    page_bases(base, blk);
+#pragma unroll
+    for (int j = 0; j < kTiles; ++j) {
+      const f16* krow = kp + base[j] + (size_t)li * D + 8 * lg;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) o.k[j][s] = *reinterpret_cast<const f16x8*>(krow + 32 * s);
+    }
+  };
+  auto load_v = [&](Blk& o, int blk) __attribute__((always_inline)) {
+    size_t base[kTiles];
+    page_bases(base, blk);
+#pragma unroll
+    for (int j = 0; j < kTiles; ++j) {
+      const f16* vrow = vp + base[j] + 8 * li;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) o.v[j][u] = *reinterpret_cast<const f16x8*>(vrow + (size_t)(4 * u + lg) * D);
+    }
+  };
+  auto load_block = [&](Blk& o, int blk) __attribute__((always_inline)) {
+    load_k(o, blk);
+    load_v(o, blk);
+  };
+  // The first block's K/V do not depend on q: issue them before the fused prologue so
+  // its latency overlaps theirs -- except in the wavefront whose block holds the new
+  // token (that one is appended by the prologue).
+  Blk A;
+  int blk = b0 + wave;
+  bool loaded = false;
+  if (qkv.part && blk < b1 && blk != (qkv.positions[b] / kBlock)) {
+    load_block(A, blk);
+    loaded = true;
+  }
+  if (pt_cached)
+    for (int i = threadIdx.x; i < pg1 - pg0; i += 64 * kWaves) sm_pt[i] = ptrow[pg0 + i];
   if (qkv.part) {  // fused decode input (q_len == 1): q, k, v of this row and KV head
     const int pos = qkv.positions[b];
     const int N = (Hq + 2 * Hkv) * D;
@@ -132,10 +201,14 @@ __global__ __launch_bounds__(64 * kWaves) void attn_f16_d128(
         if (writer && slot >= 0) vp[(((size_t)slot * Hkv + kvh) * P + off) * D + d] = static_cast<f16>(v);
       }
     }
-    // Publishes q in LDS and the appended k/v (global stores before a workgroup barrier
-    // are visible to the workgroup; no wavefront has read that page line yet).
+    // Publishes q and the page-table cache in LDS and the appended k/v (global stores
+    // before a workgroup barrier are visible to the workgroup; no wavefront has read
+    // that page line yet).
     __syncthreads();
+  } else if (pt_cached) {
+    __syncthreads();  // publishes the page-table cache
   }
+  pt_ready = true;
 
   // Q as the MFMA A operand: row li = head kvh*G + li (zero rows past G); element e
   // of step s is head dim 32*s + 8*lg + e, the same mapping the K loads use.
@@ -162,40 +235,9 @@ __global__ __launch_bounds__(64 * kWaves) void attn_f16_d128(
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[h][e] = 0.f;
 
-  // One block of K/V operands (kTiles 16-token tiles) for one wavefront.
-  struct Blk {
-    f16x8 k[kTiles][4], v[kTiles][4];
-  };
-  // Issue every K load, then every V load, of block `blk` (K first: the scores need
-  // only K, so they start while V is still arriving).  Tiles past the end re-read
-  // the block's first tile (masked in the scores).
-  auto load_block = [&](Blk& o, int blk) __attribute__((always_inline)) {
+  // Scores of block `blk`: sc[j][r] = S[head 4*lg + r][token tb + 16*j + li] (log2 units).
+  auto scores = [&](const Blk& o, int blk, f32x4 (&sc)[kTiles]) __attribute__((always_inline)) {
     const int tb = blk * kBlock;
-    size_t base[kTiles];
-#pragma unroll
-    for (int j = 0; j < kTiles; ++j) {
-      const int tj = tb + 16 * j;
-      const int tv = tj < L ? tj : tb;
-      const int page = ptrow[tv / P];
-      base[j] = (((size_t)page * Hkv + kvh) * P + (tv % P)) * D;
-    }
-#pragma unroll
-    for (int j = 0; j < kTiles; ++j) {
-      const f16* krow = kp + base[j] + (size_t)li * D + 8 * lg;
-#pragma unroll
-      for (int s = 0; s < 4; ++s) o.k[j][s] = *reinterpret_cast<const f16x8*>(krow + 32 * s);
-    }
-#pragma unroll
-    for (int j = 0; j < kTiles; ++j) {
-      const f16* vrow = vp + base[j] + 8 * li;
-#pragma unroll
-      for (int u = 0; u < 4; ++u) o.v[j][u] = *reinterpret_cast<const f16x8*>(vrow + (size_t)(4 * u + lg) * D);
-    }
-  };
-  auto compute_block = [&](const Blk& o, int blk) __attribute__((always_inline)) {
-    const int tb = blk * kBlock;
-    // Scores: sc[j][r] = S[head 4*lg + r][token tb + 16*j + li].
-    f32x4 sc[kTiles];
 #pragma unroll
     for (int j = 0; j < kTiles; ++j) {
       f32x4 c = {0.f, 0.f, 0.f, 0.f};
@@ -205,7 +247,9 @@ __global__ __launch_bounds__(64 * kWaves) void attn_f16_d128(
 #pragma unroll
       for (int r = 0; r < 4; ++r) sc[j][r] = valid ? c[r] * scale_log2 : -INFINITY;
     }
-    // Online softmax update per head row (the 16 lanes of a row share 4 heads).
+  };
+  // Online softmax update with the block's scores, then O += P V.
+  auto softmax_pv = [&](const Blk& o, f32x4 (&sc)[kTiles]) __attribute__((always_inline)) {
     float alpha[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -251,13 +295,27 @@ __global__ __launch_bounds__(64 * kWaves) void attn_f16_d128(
     }
   };
 
-  for (int blk = b0 + wave; blk < b1; blk += kWaves) {
-    Blk A;
-    load_block(A, blk);
-    // Keep all loads of the block ahead of their first use (the scheduler would
-    // otherwise interleave them with the MFMAs and leave one load in flight).
-    __builtin_amdgcn_sched_barrier(0);
-    compute_block(A, blk);
+  // Rotating pipeline: the next block's K is loaded into the K registers as soon as
+  // this block's scores have read them, and its V once P V has read this block's V,
+  // so every wavefront keeps loads in flight while it computes.  The last block is
+  // peeled off, which keeps the steady-state loads unconditional (load counters
+  // retire in order; a conditional load would make every wait a full drain).
+  {
+    const int nb = blk < b1 ? (b1 - blk + kWaves - 1) / kWaves : 0;
+    if (nb > 0) {
+      if (!loaded) load_block(A, blk);
+      f32x4 sc[kTiles];
+      for (int t = 0; t + 1 < nb; ++t, blk += kWaves) {
+        scores(A, blk, sc);
+        load_k(A, blk + kWaves);
+        __builtin_amdgcn_sched_barrier(0);
+        softmax_pv(A, sc);
+        load_v(A, blk + kWaves);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      scores(A, blk, sc);
+      softmax_pv(A, sc);
+    }
   }
 
   // Wavefront totals: O over the 4 token groups, l over the 16 lanes of a row.

@@ -542,13 +542,13 @@ void launch_qgemm_xs(const f16* x, int ldx, const uint8_t* wq, const uint16_t* w
 // Llama-3-8B shapes (m = 1, 8, 32) against NT = 4 and ring depths 2..6.
 constexpr int xs_rows_per_group(int m) { return m <= 16 ? 64 : 128; }
 
-// k-split: the smallest power of two that gives >= 256 workgroups, keeping at least
+// k-split: the smallest power of two that gives >= 192 workgroups, keeping at least
 // 4 quads per split (split-k partials cost 4*m*n bytes each, so no more than needed).
 int default_splits(int m, int n, int k) {
   const int kq = k / 128;
   const long groups = (long)((n + xs_rows_per_group(m) - 1) / xs_rows_per_group(m)) * ((m + 31) / 32);
   int s = 1;
-  while (groups * s < 256 && kq % (2 * s) == 0 && kq / (2 * s) >= 4) s *= 2;
+  while (groups * s < 192 && kq % (2 * s) == 0 && kq / (2 * s) >= 4) s *= 2;
   return s;
 }
 

@@ -17,8 +17,8 @@ every step re-appends at the same slot and attends over exactly 2048 tokens.
 Printed: one JSON line with value = decode tokens/s (32 tokens per step), the
 paged-attention roofline (algorithmic bytes / live HIP-event time of the attention
 kernel, rotated over the 32 layers' KV so the 256 MB MALL cannot hold it), the same
-for the largest projection (gate|up Q4_0 GEMM at m = batch, rotated over the 32
-layers' weights), and a CPU baseline (the C/OpenMP oracle restatement timed on this
+for the largest projection (the fused gate|up Q4_0 GEMM + SwiGLU at m = batch, rotated
+over the 32 layers' weights), and a CPU baseline (the C/OpenMP oracle restatement timed on this
 host over one layer and the lm_head, scaled to a full step).
 
 roofline.traffic is the HBM bytes per attention launch measured by rocprofv3
@@ -192,23 +192,22 @@ def main() -> int:
     achieved = attn_bytes / (attn_us * 1e-6) / 1e9
     log(f"attention {attn_us:.2f} us/launch, {achieved:.0f} GB/s ({achieved / HBM_PEAK_GBS:.1%} of peak)")
 
-    # ---- the same for the gate|up projection GEMM (m = batch), rotated over the layers' weights ----
-    gu = [base.weights.matmul_weight((f"layer{i}_gate_w", f"layer{i}_up_w")) for i in range(cfg.num_layers)]
+    # ---- the same for the fused gate|up GEMM + SwiGLU (m = batch), rotated over the layers' weights ----
+    gu = [base.weights.swiglu_weight(f"layer{i}_gate_w", f"layer{i}_up_w") for i in range(cfg.num_layers)]
     xg = torch.randn((B, cfg.hidden_size), device=dev, dtype=torch.float16)
-    g_splits = kernels.choose_splits(B, gu[0].n, gu[0].k)
-    g_out = torch.empty((g_splits, B, gu[0].n), device=dev, dtype=torch.float32)
+    g_out = torch.empty((B, gu[0].n // 2), device=dev, dtype=torch.float16)
     for i in range(4):
-        kernels.qgemm_partial(xg, gu[i % len(gu)], splits=g_splits, out=g_out)
+        kernels.qgemm_swiglu(xg, gu[i % len(gu)], out=g_out)
     torch.cuda.synchronize()
     e0.record(stream)
     for it in range(args.gemm_iters):
-        kernels.qgemm_partial(xg, gu[it % len(gu)], splits=g_splits, out=g_out)
+        kernels.qgemm_swiglu(xg, gu[it % len(gu)], out=g_out)
     e1.record(stream)
     torch.cuda.synchronize()
     gemm_us = e0.elapsed_time(e1) * 1000.0 / args.gemm_iters
-    gemm_bytes = gu[0].nbytes + 2 * B * gu[0].k + 4 * g_splits * B * gu[0].n
+    gemm_bytes = gu[0].nbytes + 2 * B * gu[0].k + 2 * B * (gu[0].n // 2)
     gemm_gbs = gemm_bytes / (gemm_us * 1e-6) / 1e9
-    log(f"gate|up GEMM {gemm_us:.2f} us/launch (m={B}, splits {g_splits}), {gemm_gbs:.0f} GB/s")
+    log(f"gate|up GEMM + SwiGLU {gemm_us:.2f} us/launch (m={B}), {gemm_gbs:.0f} GB/s")
 
     traffic = measured_traffic(TRAFFIC_FILE)
 
@@ -245,10 +244,10 @@ def main() -> int:
                      "traffic": traffic["bytes"] if traffic else None,
                      "traffic_detail": traffic,
                      "bytes_per_launch": attn_bytes, "us_per_launch": round(attn_us, 3)},
-        "roofline_gemm": {"bound": "hbm", "kernel": f"Q4_0 gate|up GEMM m={B} (qgemm_xs_kernel)",
+        "roofline_gemm": {"bound": "hbm", "kernel": f"Q4_0 gate|up GEMM + SwiGLU m={B} (qgemm_xs_kernel, EPI=1)",
                           "achieved": round(gemm_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                           "frac": round(gemm_gbs / HBM_PEAK_GBS, 4), "bytes_per_launch": gemm_bytes,
-                          "us_per_launch": round(gemm_us, 3), "splits": g_splits},
+                          "us_per_launch": round(gemm_us, 3)},
         "step_bytes": {"weights": weight_bytes, "kv": kv_bytes * cfg.num_layers,
                        "hbm_floor_ms": round((weight_bytes + kv_bytes * cfg.num_layers) / HBM_PEAK_GBS / 1e6, 4)},
         "cpu_baseline": cpu,

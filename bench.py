@@ -10,8 +10,10 @@ is a real decode step over that paged context).
 
 A "step" = one HIP-graph replay of the whole decode graph: token embedding, 32 x
 (RMSNorm + QKV GEMM + RoPE/KV-append, paged attention, O GEMM + residual, RMSNorm +
-gate|up GEMM + SwiGLU, down GEMM + residual), final norm, lm_head GEMM, argmax, and the
-copy of the argmax ids into the next step's input.  Positions are held at 2047, so
+gate|up GEMM + SwiGLU, down GEMM + residual), final norm, the lm_head GEMM fused with the
+greedy argmax (the logits are not stored), and the copy of the ids into the next step's
+input.  Before timing, one step through the unfused path (logits stored, then argmax)
+checks that both pick the same ids.  Positions are held at 2047, so
 every step re-appends at the same slot and attends over exactly 2048 tokens.
 
 Printed: one JSON line with value = decode tokens/s (32 tokens per step), the
@@ -136,8 +138,19 @@ def main() -> int:
     log(f"model ready in {time.time() - t0:.1f}s; weights {base.weights.nbytes() / 1e9:.3f} GB, "
         f"KV pool {base.kv_allocator.stats()['persistent_pools'][0]['bytes'] / 1e9:.3f} GB")
 
+    # the timed step is the greedy one (LM head fused with the argmax); check once that it picks the ids the
+    # logits path picks, and that the logits are finite
+    plan.launch_with_argmax()
+    torch.cuda.synchronize()
+    assert torch.isfinite(plan.logits).all().item(), "non-finite logits"
+    want = plan.next_ids.clone()
+    plan.next_ids.zero_()
+    plan.launch_greedy()
+    torch.cuda.synchronize()
+    assert torch.equal(plan.next_ids, want), "fused greedy head disagrees with argmax(logits)"
+
     def body():
-        plan.launch_with_argmax()
+        plan.launch_greedy()
         plan.ids.copy_(plan.next_ids)
 
     # capture (warm-up on a side stream first, as torch requires)
@@ -162,7 +175,7 @@ def main() -> int:
     torch.cuda.synchronize()
     ms_step = start.elapsed_time(end) / args.steps
     toks = B * 1000.0 / ms_step
-    assert torch.isfinite(plan.logits).all().item(), "non-finite logits"
+    assert bool(((plan.next_ids >= 0) & (plan.next_ids < cfg.vocab_size)).all().item()), "ids out of range"
     log(f"step {ms_step:.3f} ms -> {toks:.1f} tok/s")
 
     # ---- live roofline of the paged-attention kernel (HIP events on the launch stream) ----

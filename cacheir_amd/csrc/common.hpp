@@ -61,4 +61,15 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// Greedy-sampling order (numpy argmax, scheduler.py:535-543): the larger value wins,
+// NaN counts as larger than every number, and equal values go to the smaller index.
+__device__ __forceinline__ void argmax_better(float& bv, int& bi, float v, int i) {
+  const bool vn = v != v, bn = bv != bv;
+  const bool take = vn ? (!bn || i < bi) : (!bn && (v > bv || (v == bv && i < bi)));
+  if (take) {
+    bv = v;
+    bi = i;
+  }
+}
+
 }  // namespace cir

@@ -352,20 +352,32 @@ struct XsChunk {  // this thread's share of one quad of activations
   u32x4 v[MT];
 };
 
+// KG k-groups: a workgroup holds KG groups of four wavefronts on the same output
+// tiles; group g takes quads q0 + g, q0 + g + KG, ... of the split, so each SIMD runs
+// KG wavefronts and one wavefront's dequant/MFMA work overlaps another's loads.  The
+// groups' accumulators are summed through LDS in group order at the end.
 // EPI 0: store fp32 split-k partials part[split][m][n].
 // EPI 1 (SwiGLU, one split): the weight tiles alternate gate / up (tile 2c = gate
 // rows 16c.., tile 2c+1 = the matching up rows), so a wavefront with NT = 2 holds
 // both accumulators of 16 intermediate columns and writes silu(g) * u to
 // out[m][N/2] (type TO) -- the SwiGLU of cpu.py:266-279 without a partials pass.
-template <int FMT, int NT, int MT, int DW, int EPI = 0, typename TO = float>
-__global__ __launch_bounds__(256) void qgemm_xs_kernel(const f16* __restrict__ x, int ldx,
+// EPI 2 (greedy head, one split): no logits are stored; each wavefront writes, per
+// row, the best (value, column) of its NT*16 columns to cand_v / cand_i
+// [m][wavefront] (part and act reinterpreted), reduced by argmax_cand_kernel.
+template <int FMT, int NT, int MT, int DW, int EPI = 0, typename TO = float, int KG = 1>
+__global__ __launch_bounds__(256 * KG) void qgemm_xs_kernel(const f16* __restrict__ x, int ldx,
                                                        const uint8_t* __restrict__ wq, const uint16_t* __restrict__ wd,
                                                        float* __restrict__ part, int M, int N, int K,
                                                        int quads_per_split, TO* __restrict__ act = nullptr) {
-  static_assert(EPI == 0 || NT == 2, "the SwiGLU epilogue pairs tile 2c (gate) with 2c+1 (up)");
+  static_assert(EPI != 1 || NT == 2, "the SwiGLU epilogue pairs tile 2c (gate) with 2c+1 (up)");
   constexpr int LB = Stage<FMT, NT, MT>::LB;
-  __shared__ __align__(16) uint8_t xs[2][16 * MT * kXsRowBytes];
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  constexpr int kSlot = 16 * MT * kXsRowBytes;  // one quad of activations
+  // after the k loop the same memory holds groups 1..KG-1's accumulators (and row sums)
+  constexpr int kRed = (KG - 1) * 4 * (MT * NT + (is_row_fmt(FMT) ? MT : 0)) * 4 * 64 * (int)sizeof(float);
+  __shared__ __align__(16) uint8_t smem[(2 * KG * kSlot > kRed) ? 2 * KG * kSlot : kRed];
+  const int wave_all = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int kg = wave_all >> 2, wave = wave_all & 3;
+  const int tid = threadIdx.x & 255;  // thread index inside the k-group
   const int lane = threadIdx.x & 63;
   const int li = lane & 15, lg = lane >> 4;
   const int KQ = K / 128;
@@ -373,15 +385,15 @@ __global__ __launch_bounds__(256) void qgemm_xs_kernel(const f16* __restrict__ x
   const int nt0 = (blockIdx.x * 4 + wave) * NT;  // this wavefront's first tile
   const int split = blockIdx.y;
   const int m0 = blockIdx.z * 16 * MT;
-  const int q0 = split * quads_per_split;
-  const int nq = quads_per_split;
+  const int q0 = split * quads_per_split + kg;
+  const int nq = quads_per_split / KG;  // this group's quads (the host makes KG divide quads_per_split)
 
   // Cooperative activation chunk of this thread: row r = c / 16, 16-byte column c % 16.
   const f16* xsrc[MT];
   int xdst[MT];
 #pragma unroll
   for (int u = 0; u < MT; ++u) {
-    const int c = threadIdx.x + 256 * u;
+    const int c = tid + 256 * u;
     const int r = c >> 4, col = c & 15;
     xsrc[u] = x + (size_t)min(m0 + r, M - 1) * ldx + 8 * col;  // rows past M re-read row M-1 (never stored)
     xdst[u] = r * kXsRowBytes + 16 * col;
@@ -403,7 +415,7 @@ __global__ __launch_bounds__(256) void qgemm_xs_kernel(const f16* __restrict__ x
   XsChunk<MT> xc[DW];
   // (always_inline: a ring slot index must fold to a constant, or the rings go to scratch)
   auto issue = [&](int slot_w, int idx) __attribute__((always_inline)) {  // stage idx (clamped to the last quad)
-    const int Q = q0 + min(idx, nq - 1);
+    const int Q = q0 + KG * min(idx, nq - 1);
 #pragma unroll
     for (int u = 0; u < MT; ++u) xc[slot_w].v[u] = *reinterpret_cast<const u32x4*>(xsrc[u] + 128 * Q);
 #pragma unroll
@@ -416,7 +428,7 @@ __global__ __launch_bounds__(256) void qgemm_xs_kernel(const f16* __restrict__ x
   };
   auto put_x = [&](int slot_x, const XsChunk<MT>& ch) __attribute__((always_inline)) {
 #pragma unroll
-    for (int u = 0; u < MT; ++u) *reinterpret_cast<u32x4*>(&xs[slot_x][xdst[u]]) = ch.v[u];
+    for (int u = 0; u < MT; ++u) *reinterpret_cast<u32x4*>(&smem[(slot_x * KG + kg) * kSlot + xdst[u]]) = ch.v[u];
   };
   auto barrier = [] { __syncthreads(); };
 
@@ -435,7 +447,8 @@ __global__ __launch_bounds__(256) void qgemm_xs_kernel(const f16* __restrict__ x
     for (int a = 0; a < MT; ++a)
 #pragma unroll
       for (int j = 0; j < 4; ++j)
-        sg.x[a][j] = *reinterpret_cast<const f16x8*>(&xs[slot_x][(16 * a + li) * kXsRowBytes + 64 * j + 16 * lg]);
+        sg.x[a][j] = *reinterpret_cast<const f16x8*>(
+            &smem[(slot_x * KG + kg) * kSlot + (16 * a + li) * kXsRowBytes + 64 * j + 16 * lg]);
 #pragma unroll
     for (int b = 0; b < NT; ++b) {
 #pragma unroll
@@ -475,6 +488,35 @@ __global__ __launch_bounds__(256) void qgemm_xs_kernel(const f16* __restrict__ x
     }
   });
 
+  if constexpr (KG > 1) {
+    // The loop ended on a barrier after the last LDS read.  Groups 1.. park their
+    // accumulators (and row sums) in LDS; group 0 adds them in group order.
+    float* red = reinterpret_cast<float*>(smem);
+    constexpr int kVals = MT * NT + (is_row_fmt(FMT) ? MT : 0);  // f32x4 per lane
+    auto slot = [&](int g, int v, int r) { return ((((g - 1) * 4 + wave) * kVals + v) * 4 + r) * 64 + lane; };
+    if (kg > 0) {
+#pragma unroll
+      for (int a = 0; a < MT; ++a)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+#pragma unroll
+          for (int b = 0; b < NT; ++b) red[slot(kg, a * NT + b, r)] = acc[a][b][r];
+          if constexpr (is_row_fmt(FMT)) red[slot(kg, MT * NT + a, r)] = sx[a][r];
+        }
+    }
+    barrier();
+    if (kg > 0) return;
+#pragma unroll
+    for (int g = 1; g < KG; ++g)
+#pragma unroll
+      for (int a = 0; a < MT; ++a)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+#pragma unroll
+          for (int b = 0; b < NT; ++b) acc[a][b][r] += red[slot(g, a * NT + b, r)];
+          if constexpr (is_row_fmt(FMT)) sx[a][r] += red[slot(g, MT * NT + a, r)];
+        }
+  }
   if constexpr (is_row_fmt(FMT)) {
     // w = (c - zp) * s with c the stored code: acc holds sum x*c over this split, so
     // the split's share of y is s * (acc + (c0 - zp) * sum x), c0 - zp = offset[row].
@@ -490,7 +532,36 @@ __global__ __launch_bounds__(256) void qgemm_xs_kernel(const f16* __restrict__ x
         for (int r = 0; r < 4; ++r) acc[a][b][r] = sc * fmaf(of, sx[a][r], acc[a][b][r]);
     }
   }
-  if constexpr (EPI == 1) {
+  if constexpr (EPI == 2) {
+    float* cand_v = part;
+    int* cand_i = reinterpret_cast<int*>(act);
+    const int wv_global = blockIdx.x * 4 + wave;
+    const int W = gridDim.x * 4;
+#pragma unroll
+    for (int a = 0; a < MT; ++a)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float bv = -INFINITY;
+        int bi = 0x7fffffff;
+#pragma unroll
+        for (int b = 0; b < NT; ++b) {
+          const int n = (nt0 + b) * 16 + li;
+          if (nt0 + b < NTILES && n < N) argmax_better(bv, bi, acc[a][b][r], n);
+        }
+        // the 16 lanes of this row group (same lg) hold 16 different columns
+#pragma unroll
+        for (int off = 8; off > 0; off >>= 1) {
+          const float ov = __shfl_xor(bv, off, 64);
+          const int oi = __shfl_xor(bi, off, 64);
+          argmax_better(bv, bi, ov, oi);
+        }
+        const int m = m0 + 16 * a + 4 * lg + r;
+        if (li == 0 && m < M) {
+          cand_v[(size_t)m * W + wv_global] = bv;
+          cand_i[(size_t)m * W + wv_global] = bi;
+        }
+      }
+  } else if constexpr (EPI == 1) {
     const int inter = N / 2;
     const int col = (nt0 >> 1) * 16 + li;
     if (nt0 + 1 < NTILES && col < inter) {
@@ -520,12 +591,96 @@ __global__ __launch_bounds__(256) void qgemm_xs_kernel(const f16* __restrict__ x
   }
 }
 
+#ifndef CIR_XS_DW
+#define CIR_XS_DW 4
+#endif
+#ifndef CIR_XS_DW_SWIGLU
+#define CIR_XS_DW_SWIGLU 4
+#endif
+#ifndef CIR_XS_KG
+#define CIR_XS_KG 1
+#endif
+
+// k-groups per workgroup: m > 16 only, and a divisor of the split's quad count.
+// qgemm (splits 1) and the fused SwiGLU pick the same value for the same k, so
+// their sums run in the same order.
+int xs_kgroups(int m, int quads) {
+  int kg = m > 16 ? CIR_XS_KG : 1;
+  while (kg > 1 && quads % kg) kg /= 2;
+  return kg;
+}
+
 template <int FMT, int MT, typename TO>
 void launch_qgemm_swiglu(const f16* x, int ldx, const uint8_t* wq, const uint16_t* wd, TO* act, int M, int N, int K,
                          hipStream_t s) {
   const int NTILES = (N + 15) / 16;
   dim3 grid((NTILES + 7) / 8, 1, (M + 16 * MT - 1) / (16 * MT));
-  qgemm_xs_kernel<FMT, 2, MT, 4, 1, TO><<<grid, 256, 0, s>>>(x, ldx, wq, wd, nullptr, M, N, K, K / 128, act);
+  auto go = [&]<int KG>() {
+    qgemm_xs_kernel<FMT, 2, MT, CIR_XS_DW_SWIGLU, 1, TO, KG>
+        <<<grid, 256 * KG, 0, s>>>(x, ldx, wq, wd, nullptr, M, N, K, K / 128, act);
+  };
+  const int kg = xs_kgroups(M, K / 128);
+  if constexpr (CIR_XS_KG >= 4) {
+    if (kg == 4) return go.template operator()<4>();
+  }
+  if (kg == 2) go.template operator()<2>();
+  else go.template operator()<1>();
+}
+
+// ids[m] = best candidate of row m over the W wavefront candidates (any order: the
+// candidates carry their columns, so ties resolve to the smallest column).
+__global__ __launch_bounds__(256) void argmax_cand_kernel(const float* __restrict__ cand_v, const int* __restrict__ cand_i,
+                                                          int W, int M, int64_t* __restrict__ ids) {
+  __shared__ float sv[4];
+  __shared__ int si[4];
+  const int m = blockIdx.x;
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
+  const float* cv = cand_v + (size_t)m * W;
+  const int* ci = cand_i + (size_t)m * W;
+  for (int w = threadIdx.x; w < W; w += 256) argmax_better(bv, bi, cv[w], ci[w]);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const float ov = __shfl_xor(bv, off, 64);
+    const int oi = __shfl_xor(bi, off, 64);
+    argmax_better(bv, bi, ov, oi);
+  }
+  if ((threadIdx.x & 63) == 0) {
+    sv[threadIdx.x >> 6] = bv;
+    si[threadIdx.x >> 6] = bi;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+#pragma unroll
+    for (int w = 1; w < 4; ++w) argmax_better(bv, bi, sv[w], si[w]);
+    ids[m] = bi == 0x7fffffff ? 0 : bi;
+  }
+}
+
+// Wavefront candidates of the fused head: one per 64*NT columns and row.
+constexpr int xs_rows_per_wave(int m) { return m <= 16 ? 16 : 32; }
+size_t argmax_cand_count(int m, int n) {
+  const int rows_per_group = 4 * xs_rows_per_wave(m);
+  return (size_t)((n + rows_per_group - 1) / rows_per_group) * 4 * m;
+}
+
+template <int FMT, int NT, int MT>
+void launch_qgemm_argmax(const f16* x, int ldx, const uint8_t* wq, const uint16_t* wd, float* cand_v, int* cand_i,
+                         int64_t* ids, int M, int N, int K, hipStream_t s) {
+  const int NTILES = (N + 15) / 16;
+  dim3 grid((NTILES + 4 * NT - 1) / (4 * NT), 1, (M + 16 * MT - 1) / (16 * MT));
+  const int quads = K / 128;
+  auto go = [&]<int KG>() {
+    qgemm_xs_kernel<FMT, NT, MT, (MT == 1 ? 4 : CIR_XS_DW), 2, float, KG>
+        <<<grid, 256 * KG, 0, s>>>(x, ldx, wq, wd, cand_v, M, N, K, quads, reinterpret_cast<float*>(cand_i));
+  };
+  const int kg = MT == 1 ? 1 : xs_kgroups(M, quads);
+  if constexpr (CIR_XS_KG >= 4) {
+    if (kg == 4) return go.template operator()<4>(), argmax_cand_kernel<<<M, 256, 0, s>>>(cand_v, cand_i, (int)grid.x * 4, M, ids);
+  }
+  if (kg == 2) go.template operator()<2>();
+  else go.template operator()<1>();
+  argmax_cand_kernel<<<M, 256, 0, s>>>(cand_v, cand_i, (int)grid.x * 4, M, ids);
 }
 
 template <int FMT, int NT, int MT, int DW>
@@ -533,7 +688,20 @@ void launch_qgemm_xs(const f16* x, int ldx, const uint8_t* wq, const uint16_t* w
                      int splits, hipStream_t s) {
   const int NTILES = (N + 15) / 16;
   dim3 grid((NTILES + 4 * NT - 1) / (4 * NT), splits, (M + 16 * MT - 1) / (16 * MT));
-  qgemm_xs_kernel<FMT, NT, MT, DW><<<grid, 256, 0, s>>>(x, ldx, wq, wd, part, M, N, K, (K / 128) / splits);
+  const int quads = (K / 128) / splits;
+  auto go = [&]<int KG>() {
+    qgemm_xs_kernel<FMT, NT, MT, DW, 0, float, KG><<<grid, 256 * KG, 0, s>>>(x, ldx, wq, wd, part, M, N, K, quads);
+  };
+  const int kg = xs_kgroups(M, quads);
+  if constexpr (MT == 1) {
+    go.template operator()<1>();
+  } else {
+    if constexpr (CIR_XS_KG >= 4) {
+      if (kg == 4) return go.template operator()<4>();
+    }
+    if (kg == 2) go.template operator()<2>();
+    else go.template operator()<1>();
+  }
 }
 
 // Workgroup rows: 4 wavefronts x NT tiles x 16.  m <= 16 takes NT = 1 (64 rows per
@@ -556,7 +724,7 @@ template <int FMT>
 void dispatch_qgemm(const f16* x, int ldx, const uint8_t* wq, const uint16_t* wd, float* part, int M, int N, int K,
                     int splits, hipStream_t s) {
   if (M <= 16) launch_qgemm_xs<FMT, 1, 1, 4>(x, ldx, wq, wd, part, M, N, K, splits, s);
-  else launch_qgemm_xs<FMT, 2, 2, 4>(x, ldx, wq, wd, part, M, N, K, splits, s);
+  else launch_qgemm_xs<FMT, 2, 2, CIR_XS_DW>(x, ldx, wq, wd, part, M, N, K, splits, s);
 }
 
 }  // namespace
@@ -702,5 +870,40 @@ extern "C" int cir_gemm_f32(const float* x, int ldx, const float* w, float* y_pa
   const int kc = (k + splits - 1) / splits;
   dim3 grid((n + 3) / 4, splits);
   gemm_f32_kernel<<<grid, 256, 0, as_stream(stream)>>>(x, ldx, w, y_partial, m, n, k, kc);
+  return launch_status();
+}
+
+extern "C" size_t cir_qgemm_argmax_workspace_bytes(int m, int n) {
+  if (m <= 0 || n <= 0) return 0;
+  return cir::argmax_cand_count(m, n) * (sizeof(float) + sizeof(int));
+}
+
+extern "C" int cir_qgemm_argmax(const void* x, int ldx, const void* w_tiled, int fmt, int64_t* ids, void* workspace,
+                                size_t ws_bytes, int m, int n, int k, void* stream) {
+  CIR_CHECK_ARG(valid_fmt(fmt), "qgemm_argmax: unknown weight format %d", fmt);
+  CIR_CHECK_ARG(m >= 0 && n > 0 && k >= 0, "qgemm_argmax: bad sizes (m %d, n %d)", m, n);
+  if (m == 0) return 0;
+  CIR_CHECK_ARG(k > 0 && k % 128 == 0, "qgemm_argmax: k (%d) must be a positive multiple of 128", k);
+  CIR_CHECK_ARG(ldx >= k && ldx % 8 == 0, "qgemm_argmax: ldx (%d) must be >= k and a multiple of 8", ldx);
+  CIR_CHECK_ARG(x && w_tiled && ids && workspace, "qgemm_argmax: null pointer");
+  CIR_CHECK_ARG(m <= 65535 && (m + 15) / 16 <= 65535, "qgemm_argmax: m (%d) too large", m);
+  const size_t cand = cir::argmax_cand_count(m, n);
+  CIR_CHECK_ARG(ws_bytes >= cand * (sizeof(float) + sizeof(int)), "qgemm_argmax: workspace needs %zu bytes (got %zu)",
+                cand * (sizeof(float) + sizeof(int)), ws_bytes);
+  const size_t tiles = (size_t)((n + 15) / 16) * (k / 128);
+  const uint8_t* q = static_cast<const uint8_t*>(w_tiled);
+  const uint16_t* d = reinterpret_cast<const uint16_t*>(q + tiles * 64 * quant_bytes_per_lane(fmt));
+  const f16* xh = static_cast<const f16*>(x);
+  float* cv = static_cast<float*>(workspace);
+  int* ci = reinterpret_cast<int*>(cv + cand);
+  hipStream_t s = as_stream(stream);
+  auto go = [&]<int FMT>() {
+    if (m <= 16) launch_qgemm_argmax<FMT, 1, 1>(xh, ldx, q, d, cv, ci, ids, m, n, k, s);
+    else launch_qgemm_argmax<FMT, 2, 2>(xh, ldx, q, d, cv, ci, ids, m, n, k, s);
+  };
+  if (fmt == CIR_Q4_0) go.template operator()<CIR_Q4_0>();
+  else if (fmt == CIR_Q8_0) go.template operator()<CIR_Q8_0>();
+  else if (fmt == CIR_I4_ROW) go.template operator()<CIR_I4_ROW>();
+  else go.template operator()<CIR_I8_ROW>();
   return launch_status();
 }

@@ -260,12 +260,7 @@ __global__ void epi_qkv_kernel(const float* __restrict__ part, int splits, const
 }
 
 // ---------------------------------------------------------------- argmax -----
-__device__ __forceinline__ void better(float& bv, int& bi, float v, int i) {
-  if (v > bv || (v == bv && i < bi)) {
-    bv = v;
-    bi = i;
-  }
-}
+__device__ __forceinline__ void better(float& bv, int& bi, float v, int i) { argmax_better(bv, bi, v, i); }
 
 __global__ __launch_bounds__(kRowThreads) void argmax_kernel(const float* __restrict__ logits, int ld,
                                                              int64_t* __restrict__ ids, int vocab) {

@@ -46,6 +46,8 @@ _SIGNATURES = {
     "cir_qgemm_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int]),
     "cir_qgemm": (_c_int, [_vp, _c_int, _vp, _c_int, _vp, _c_int, _c_int, _c_int, _c_int, _vp]),
     "cir_qgemm_swiglu": (_c_int, [_vp, _c_int, _vp, _c_int, _vp, _c_int, _c_int, _c_int, _c_int, _vp]),
+    "cir_qgemm_argmax_workspace_bytes": (_c_size, [_c_int, _c_int]),
+    "cir_qgemm_argmax": (_c_int, [_vp, _c_int, _vp, _c_int, _vp, _vp, _c_size, _c_int, _c_int, _c_int, _vp]),
     "cir_gemm_f32": (_c_int, [_vp, _c_int, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp]),
     "cir_epilogue_store": (_c_int, [_vp, _c_int, _vp, _vp, _c_int, _c_int, _c_int, _vp]),
     "cir_epilogue_residual_rmsnorm": (_c_int, [_vp, _c_int, _vp, _vp, _vp, _c_int, _c_float, _vp, _c_int, _c_int,

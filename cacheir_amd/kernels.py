@@ -239,6 +239,28 @@ def qgemm_swiglu(x: torch.Tensor, w: QWeight, out_dtype: torch.dtype = torch.flo
     return out
 
 
+def qgemm_argmax_workspace(m: int, n: int, device) -> torch.Tensor:
+    return torch.empty(max(hip.size_call("cir_qgemm_argmax_workspace_bytes", m, n), 4), dtype=torch.uint8,
+                       device=device)
+
+
+def qgemm_argmax(x: torch.Tensor, w: QWeight, out=None, workspace=None) -> torch.Tensor:
+    """Greedy ids ``argmax_j (x @ W^T)[r, j]`` without storing the logits (first index on ties, NaN as the
+    maximum); equal to ``argmax(qgemm_partial(x, w, splits=1)[0])``."""
+    _cuda(x, "x", rows_only=True)
+    _req(x.dtype == torch.float16, "qgemm activations must be float16", TypeError)
+    _req(x.dim() == 2 and x.shape[1] == w.k, f"x must be [m, {w.k}]")
+    m = x.shape[0]
+    if out is None:
+        out = torch.empty(m, dtype=torch.int64, device=x.device)
+    _req(out.dtype == torch.int64 and out.numel() == m and out.is_contiguous(), "out must be int64 [m]", TypeError)
+    if workspace is None:
+        workspace = qgemm_argmax_workspace(m, w.n, x.device)
+    hip.call("cir_qgemm_argmax", x.data_ptr(), x.stride(0), w.tiled.data_ptr(), w.fmt, out.data_ptr(),
+             workspace.data_ptr(), workspace.numel() * workspace.element_size(), m, w.n, w.k, hip.stream_handle())
+    return out
+
+
 def gemm_f32_partial(x: torch.Tensor, w: torch.Tensor, splits: int = 1, out=None) -> torch.Tensor:
     _cuda(x, "x")
     _cuda(w, "w")

@@ -165,6 +165,8 @@ class StepPlan:
         self.page_table = torch.zeros((batch, max_pages), dtype=torch.int32, device=dev)
         self.launches: list = []
         self.graph_obj: torch.cuda.CUDAGraph | None = None
+        self._head: tuple | None = None  # (x, lm_head weight, workspace) when the greedy head can be fused
+        self._head_at = 0
         self._gemm_need = 1
         self._build(rt.artifact.graph(mode))
         self.gemm_ws = torch.empty(self._gemm_need, dtype=torch.float32, device=dev)
@@ -301,6 +303,12 @@ class StepPlan:
                 env[outs[0]] = out
             elif op in _MATMUL_OPS:
                 W = rt.weights.matmul_weight((ins[1],))
+                if outs[0] == self.logits_name and isinstance(W, kernels.QWeight):
+                    # greedy steps may replace this GEMM + store by the fused head (cir_qgemm_argmax)
+                    x16 = as_dtype(env[ins[0]], torch.float16)
+                    self._head_at = len(self.launches)
+                    self._head = (x16, W, kernels.qgemm_argmax_workspace(rows, W.n, rt.device))
+                    env[ins[0]] = x16
                 part, _, n = gemm(env[ins[0]], W)
                 users = consumers.get(outs[0], [])
                 fuse = (len(users) == 1 and users[0].op == "add" and outs[0] in users[0].inputs
@@ -398,9 +406,21 @@ class StepPlan:
         self.launch()
         kernels.argmax(self.logits, out=self.next_ids)
 
-    def capture(self, with_argmax: bool = True) -> torch.cuda.CUDAGraph:
-        """Capture the step into a HIP graph (after one eager warm-up on a side stream)."""
-        body = self.launch_with_argmax if with_argmax else self.launch
+    def launch_greedy(self) -> None:
+        """The step up to the final norm, then the LM head fused with the argmax: next_ids is set, the logits
+        buffer is not written.  Falls back to ``launch_with_argmax`` for a dense (fp32) head."""
+        if self._head is None:
+            self.launch_with_argmax()
+            return
+        for fn in self.launches[: self._head_at]:
+            fn()
+        x, w, ws = self._head
+        kernels.qgemm_argmax(x, w, out=self.next_ids, workspace=ws)
+
+    def capture(self, with_argmax: bool = True, greedy: bool = False) -> torch.cuda.CUDAGraph:
+        """Capture the step into a HIP graph (after one eager warm-up on a side stream).  ``greedy`` captures
+        ``launch_greedy`` (ids only); otherwise the logits, plus the argmax when ``with_argmax``."""
+        body = self.launch_greedy if greedy else (self.launch_with_argmax if with_argmax else self.launch)
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(side):
@@ -534,7 +554,8 @@ class HipRuntime:
     def _dtype_name(self) -> str:
         return "float16" if self.dtype == torch.float16 else "float32"
 
-    def _execute(self, sessions: list["HipRuntime"], ids: np.ndarray, mode: str) -> torch.Tensor:
+    def _prepare(self, sessions: list["HipRuntime"], ids: np.ndarray, mode: str) -> "StepPlan":
+        """Reserve and map the KV pages the step writes, and load the step inputs into its plan."""
         batch, q_len = ids.shape
         P = self.kv_allocator.page_size
         need_pages = sum(max(0, -(-(s.kv_cache.tokens + q_len) // P) - len(s.kv_cache.slots)) for s in sessions)
@@ -550,6 +571,16 @@ class HipRuntime:
         try:
             plan = self.plan(mode, batch, q_len, max_pages)
             plan.set_inputs(ids, rows, positions)
+        except torch.cuda.OutOfMemoryError as exc:
+            self._recover_from_oom()
+            raise RuntimeError("CacheIR HIP runtime recovered from an out-of-memory condition; "
+                               "retry with a smaller batch/context") from exc
+        return plan
+
+    def _execute(self, sessions: list["HipRuntime"], ids: np.ndarray, mode: str) -> torch.Tensor:
+        batch, q_len = ids.shape
+        plan = self._prepare(sessions, ids, mode)
+        try:
             plan.launch()
         except torch.cuda.OutOfMemoryError as exc:
             self._recover_from_oom()
@@ -648,13 +679,31 @@ class HipRuntime:
         self.kv_allocator.share(slots)
         self.prefix_cache.put(ids, PrefixPages(self.kv_allocator, slots, len(ids)))
 
+    def decode_greedy(self, sessions: list["HipRuntime"], token_ids) -> list[int]:
+        """One decode step for ``sessions`` (one token each) returning the greedy next ids instead of logits
+        (``run_decode_batch`` + argmax of scheduler.py:535-543, with the LM head and argmax fused)."""
+        ids = np.asarray(token_ids, dtype=np.int64).reshape(len(sessions), 1)
+        plan = self._prepare(sessions, ids, "decode")
+        try:
+            plan.launch_greedy()
+        except torch.cuda.OutOfMemoryError as exc:
+            self._recover_from_oom()
+            raise RuntimeError("CacheIR HIP runtime recovered from an out-of-memory condition; "
+                               "retry with a smaller batch/context") from exc
+        for s in sessions:
+            s.kv_cache.tokens += 1
+        return [int(v) % self.config.vocab_size for v in plan.next_ids.cpu().tolist()]
+
     def generate_ids(self, prompt_ids, max_new_tokens: int = 16) -> list[int]:
         logits = self.run([list(prompt_ids)], mode="prefill", reset_kv=True)
         out = []
-        for _ in range(max_new_tokens):
-            nxt = int(torch.argmax(logits[0, -1]).item()) % self.config.vocab_size
+        if max_new_tokens <= 0:
+            return out
+        nxt = int(torch.argmax(logits[0, -1]).item()) % self.config.vocab_size
+        out.append(nxt)
+        for _ in range(max_new_tokens - 1):
+            nxt = self.decode_greedy([self], [nxt])[0]
             out.append(nxt)
-            logits = self.run([[nxt]], mode="decode")
         return out
 
     def generate(self, prompt: str, *, max_new_tokens: int = 16, use_prefix_cache: bool = False,

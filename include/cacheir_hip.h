@@ -198,8 +198,19 @@ int cir_add(const void* a, const void* b, void* out, int dt, size_t count, void*
 int cir_cast(const void* in, int idt, void* out, int odt, size_t count, void* stream);
 
 /* Greedy sampling (cpu.py:181-182, scheduler.py:535-543): ids[r] = first index of
- * the maximum of logits[r][0:vocab] (fp32, row stride ld). */
+ * the maximum of logits[r][0:vocab] (fp32, row stride ld); NaN counts as the maximum,
+ * as in numpy's argmax. */
 int cir_argmax(const float* logits, int ld, int64_t* ids, int rows, int vocab, void* stream);
+
+/* LM head + greedy sampling in one pass (the lm_head matmul of cuda.py:851-852 /
+ * cpu.py:256-257 followed by the argmax of scheduler.py:535-543): ids[r] = argmax over
+ * j < n of (x[r] . W[j]) for the tiled weight W [n, k], without storing the logits.
+ * The logits are computed exactly as cir_qgemm with splits = 1 computes them, so the
+ * ids equal cir_argmax over that GEMM's output.  workspace: caller-owned device memory
+ * of cir_qgemm_argmax_workspace_bytes(m, n) bytes for per-wavefront candidates. */
+size_t cir_qgemm_argmax_workspace_bytes(int m, int n);
+int cir_qgemm_argmax(const void* x, int ldx, const void* w_tiled, int fmt, int64_t* ids, void* workspace,
+                     size_t ws_bytes, int m, int n, int k, void* stream);
 
 #ifdef __cplusplus
 }

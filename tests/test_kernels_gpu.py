@@ -426,3 +426,48 @@ def test_row_kernels(device):
     logits[1, 10] = logits[1, 20] = 50.0  # tie -> first index
     got = kernels.argmax(to_dev(logits, device)).cpu().numpy()
     assert np.array_equal(got, ops.greedy(logits, 1000))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("fmt", ["q4_0", "q8_0", "i4_row", "i8_row"])
+@pytest.mark.parametrize("m", [1, 5, 16, 17, 32])
+def test_qgemm_argmax_matches_gemm_then_argmax(device, fmt, m):
+    """cir_qgemm_argmax (LM head + greedy argmax, no logits stored) == the oracle's greedy pick over the logits
+    of cir_qgemm (splits 1): bitwise the same ids, with a planted tie between a near and a far column (first
+    index wins), a row of NaN logits (numpy picks the first NaN, index 0) and a ragged vocabulary."""
+    from cacheir_amd import kernels
+
+    rng = np.random.default_rng(17 * m + len(fmt))
+    n, k = 1000, 256  # n not a multiple of the 32- or 64-column wavefront groups
+    if fmt in ("q4_0", "q8_0"):
+        enc = quant.random_q4_0 if fmt == "q4_0" else quant.random_q8_0
+        blocks = enc(rng, n, k)[0].reshape(n, -1)
+        # rows 3 and n-2: identical and dominant for positive x
+        bb = 18 if fmt == "q4_0" else 34
+        dom = np.zeros((k // 32, bb), np.uint8)
+        dom[:, :2] = np.frombuffer(np.float16(0.5).tobytes(), np.uint8)
+        dom[:, 2:] = 0xFF if fmt == "q4_0" else 0x7F
+        blocks[3] = blocks[n - 2] = dom.reshape(-1)
+        w = kernels.QWeight.from_blocks(to_dev(blocks.reshape(-1), device), kernels.FMT_NAMES[fmt], n, k)
+    else:
+        bits = 4 if fmt == "i4_row" else 8
+        wf = rng.standard_normal((n, k)).astype(np.float32) * 0.05
+        wf[3] = wf[n - 2] = np.linspace(0.4, 0.6, k, dtype=np.float32)
+        pk = quant.asymmetric_pack(wf, bits)
+        w = kernels.QWeight.from_rows(to_dev(pk["packed_values"], device), to_dev(pk["scales"], device),
+                                      to_dev(pk["zero_points"], device), bits, n, k)
+    x = np.abs(rng.standard_normal((m, k))).astype(np.float16)
+    if m > 2:
+        x[1] = rng.standard_normal(k).astype(np.float16)  # a row with an ordinary (random) winner
+    if m > 4:
+        x[4, 7] = np.float16(np.nan)  # every logit of row 4 is NaN
+    xd = to_dev(x, device)
+    logits = kernels.qgemm_partial(xd, w, splits=1)[0]
+    want = ops.greedy(logits.cpu().numpy(), n)
+    got = kernels.qgemm_argmax(xd, w).cpu().numpy()
+    assert np.array_equal(got, want), (got, want)
+    assert got[0] == 3  # tie between columns 3 and n-2 goes to the first
+    if m > 4:
+        assert got[4] == 0
+    # the fused kernel's ids also equal cir_argmax over the same logits
+    assert np.array_equal(kernels.argmax(logits).cpu().numpy(), want)

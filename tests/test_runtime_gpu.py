@@ -288,3 +288,49 @@ def test_reference_row_packed_model_matches_oracle(tmp_path, device, quant_name)
         close16(g, orc.run([[tok]], mode="decode"))
         tok = int(np.argmax(g[0, -1]))
     assert rt.kernel_counts.get("rocm.qgemm_swiglu", 0) > 0
+
+
+def test_greedy_step_fuses_head_and_argmax(tmp_path, device):
+    """decode_greedy (LM head fused with the argmax, no logits written) returns the greedy ids of
+    run_decode_batch's logits, and a captured greedy graph replays them; generate_ids (which decodes through
+    decode_greedy) matches the reference tiny-model ids computed from logits."""
+    from cacheir_amd.runtime import HipRuntime
+
+    cfg, w, blocks, decoded = _q4_model(tmp_path, "q4_0")
+    art = compile_config(cfg, quant="q4_0", model_path=str(write_model(tmp_path / "g", cfg, w)))
+    base = HipRuntime(art)
+    sessions = [base.fork() for _ in range(3)]
+    for i, s in enumerate(sessions):
+        s.run([list(range(3 + i, 20 + 3 * i))], mode="prefill")
+    logits = base.run_decode_batch(sessions, [4, 5, 6]).cpu().numpy()
+    want = [int(np.argmax(r[-1])) % cfg.vocab_size for r in logits]
+    for s in sessions:
+        s.kv_cache.tokens -= 1
+    assert base.decode_greedy(sessions, [4, 5, 6]) == want
+    for s in sessions:
+        s.kv_cache.tokens -= 1
+    plan = base.plan("decode", 3, 1, base._bucket(max(len(s.kv_cache.slots) for s in sessions)))
+    assert plan._head is not None
+    rows = np.zeros((3, plan.max_pages), np.int32)
+    for b, s in enumerate(sessions):
+        rows[b, : len(s.kv_cache.slots)] = s.kv_cache.slots
+    plan.set_inputs(np.array([[4], [5], [6]]), rows, np.array([s.kv_cache.tokens for s in sessions]))
+    plan.capture(greedy=True)
+    for _ in range(3):
+        plan.next_ids.zero_()
+        plan.replay()
+        torch.cuda.synchronize()
+        assert plan.next_ids.cpu().tolist() == want
+        _ = torch.ones(1024, device=device).sum().item()  # eager work between replays
+    # generate_ids: first id from the prefill logits, the rest through decode_greedy
+    prompt = list(range(5, 21))
+    fresh = HipRuntime(art)
+    got = fresh.generate_ids(prompt, max_new_tokens=6)
+    ref_rt = HipRuntime(art)
+    lg = ref_rt.run([prompt], mode="prefill", reset_kv=True)
+    ref = []
+    for _ in range(6):
+        nxt = int(torch.argmax(lg[0, -1]).item()) % cfg.vocab_size
+        ref.append(nxt)
+        lg = ref_rt.run([[nxt]], mode="decode")
+    assert got == ref

@@ -66,10 +66,8 @@ __device__ __forceinline__ float wave_max(float v) {
 __device__ __forceinline__ void argmax_better(float& bv, int& bi, float v, int i) {
   const bool vn = v != v, bn = bv != bv;
   const bool take = vn ? (!bn || i < bi) : (!bn && (v > bv || (v == bv && i < bi)));
-  if (take) {
-    bv = v;
-    bi = i;
-  }
+  bv = take ? v : bv;  // selects, not a branch: callers run this between lane shuffles
+  bi = take ? i : bi;
 }
 
 }  // namespace cir

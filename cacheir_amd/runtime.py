@@ -197,10 +197,11 @@ class StepPlan:
         def input_dtype_for(value: str) -> torch.dtype | None:
             """The dtype the first matmul-family consumer of ``value`` wants, if any."""
             for c in consumers.get(value, []):
+                # decided from the weight format, without packing a weight the plan may never use
                 if c.op in _MATMUL_OPS:
-                    return gemm_dtype(rt.weights.matmul_weight((c.inputs[1],)))
+                    return torch.float16 if rt.weights.is_blocked((c.inputs[1],)) else torch.float32
                 if c.op in _SWIGLU_OPS:
-                    return gemm_dtype(rt.weights.matmul_weight((c.inputs[1], c.inputs[2])))
+                    return torch.float16 if rt.weights.is_blocked((c.inputs[1], c.inputs[2])) else torch.float32
             return None
 
         def buf(n: int, dtype: torch.dtype) -> torch.Tensor:

@@ -18,8 +18,9 @@ every step re-appends at the same slot and attends over exactly 2048 tokens.
 
 Printed: one JSON line with value = decode tokens/s (32 tokens per step), the
 paged-attention roofline (algorithmic bytes / live HIP-event time of the attention
-kernel, rotated over the 32 layers' KV so the 256 MB MALL cannot hold it), the same
-for the largest projection (the fused gate|up Q4_0 GEMM + SwiGLU at m = batch, rotated
+kernel, launches captured in a HIP graph so no host gap is timed, rotated over the 32
+layers' KV so the 256 MB MALL cannot hold it), the same for the largest projection (the
+fused gate|up Q4_0 GEMM + SwiGLU at m = batch, rotated
 over the 32 layers' weights), and a CPU baseline (the C/OpenMP oracle restatement timed on this
 host over one layer and the lm_head, scaled to a full step).
 
@@ -84,6 +85,35 @@ def llama3_8b(layers: int):
     return ModelConfig(architecture="Llama3-8B-shape", hidden_size=4096, intermediate_size=14336, num_layers=layers,
                        num_attention_heads=32, num_key_value_heads=8, vocab_size=128256,
                        max_position_embeddings=8192, rope_theta=500000.0, rms_norm_eps=1e-5, dtype="float16")
+
+
+def graph_us_per_launch(launch, iters: int, replays: int = 3) -> float:
+    """GPU time per launch of ``launch(i)``: ``iters`` launches captured in one HIP graph, replayed ``replays`` times
+    between HIP events on the launch stream (no host launch gaps inside the timed region)."""
+    import torch
+
+    for i in range(4):
+        launch(i)
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        launch(0)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(iters):
+            launch(i)
+    graph.replay()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(replays):
+        graph.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1000.0 / (iters * replays)
 
 
 def log(msg: str) -> None:
@@ -185,19 +215,11 @@ def main() -> int:
     q = torch.randn((B, H, D), device=dev, dtype=torch.float16)
     out = torch.empty_like(q)
     ws = kernels.attention_workspace(B, H, D, max_pages * P, dev)
-    stream = torch.cuda.current_stream()
-    for layer in range(min(4, cfg.num_layers)):
-        kp, vp = base.kv_allocator.layer_pools(layer)
-        kernels.paged_decode_attention(q, kp, vp, plan.page_table, plan.seq_lens, out=out, workspace=ws)
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    e0.record(stream)
-    for it in range(args.attn_iters):
+    def attn(it):
         kp, vp = base.kv_allocator.layer_pools(it % cfg.num_layers)
         kernels.paged_decode_attention(q, kp, vp, plan.page_table, plan.seq_lens, out=out, workspace=ws)
-    e1.record(stream)
-    torch.cuda.synchronize()
-    attn_us = e0.elapsed_time(e1) * 1000.0 / args.attn_iters
+
+    attn_us = graph_us_per_launch(attn, args.attn_iters)
     kv_bytes = 2 * Hkv * D * 2 * B * ctx  # K + V fp16 over every visible token
     qo_bytes = 2 * B * H * D * 2
     table_bytes = 4 * B * pages_per_seq + 4 * B
@@ -209,15 +231,7 @@ def main() -> int:
     gu = [base.weights.swiglu_weight(f"layer{i}_gate_w", f"layer{i}_up_w") for i in range(cfg.num_layers)]
     xg = torch.randn((B, cfg.hidden_size), device=dev, dtype=torch.float16)
     g_out = torch.empty((B, gu[0].n // 2), device=dev, dtype=torch.float16)
-    for i in range(4):
-        kernels.qgemm_swiglu(xg, gu[i % len(gu)], out=g_out)
-    torch.cuda.synchronize()
-    e0.record(stream)
-    for it in range(args.gemm_iters):
-        kernels.qgemm_swiglu(xg, gu[it % len(gu)], out=g_out)
-    e1.record(stream)
-    torch.cuda.synchronize()
-    gemm_us = e0.elapsed_time(e1) * 1000.0 / args.gemm_iters
+    gemm_us = graph_us_per_launch(lambda it: kernels.qgemm_swiglu(xg, gu[it % len(gu)], out=g_out), args.gemm_iters)
     gemm_bytes = gu[0].nbytes + 2 * B * gu[0].k + 2 * B * (gu[0].n // 2)
     gemm_gbs = gemm_bytes / (gemm_us * 1e-6) / 1e9
     log(f"gate|up GEMM + SwiGLU {gemm_us:.2f} us/launch (m={B}), {gemm_gbs:.0f} GB/s")

@@ -120,36 +120,54 @@ __global__ __launch_bounds__(kRowThreads) void residual_rmsnorm_kernel(
   __shared__ float scratch[kRowThreads / 64];
   const int r = blockIdx.x;
   const size_t plane = (size_t)M * N;
+  // Every load of the thread (partials of both column groups, residual, norm weights) is
+  // issued before the first add, so the row costs one memory round trip; the second
+  // group exists only for rows longer than 4 * kRowThreads (uniform branch).
+  const bool second = N > 4 * kRowThreads;
+  float4 pv[2][SMAX], q[2], wv[2];
+  size_t idx[2];
+  bool ok[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int c = 4 * (threadIdx.x + i * kRowThreads);
+    ok[i] = c < N;
+    const int cc = ok[i] ? c : 0;
+    idx[i] = (size_t)r * N + cc;
+    if (i == 0 || second) {
+#pragma unroll
+      for (int sp = 0; sp < SMAX; ++sp)
+        pv[i][sp] = *reinterpret_cast<const float4*>(part + (sp < splits ? sp : 0) * plane + idx[i]);
+      q[i] = *reinterpret_cast<const float4*>(resid + idx[i]);
+      wv[i] = load4(w + cc);
+    }
+  }
   float4 v[2];
   float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
-    const int c = 4 * (threadIdx.x + i * kRowThreads);
     float4 t = {0.f, 0.f, 0.f, 0.f};
-    if (c < N) {
-      const size_t idx = (size_t)r * N + c;
-      const float4 p = split_sum4<SMAX>(part, splits, plane, idx);
-      const float4 q = *reinterpret_cast<const float4*>(resid + idx);
-      t = make_float4(q.x + p.x, q.y + p.y, q.z + p.z, q.w + p.w);
-      *reinterpret_cast<float4*>(h_out + idx) = t;
+    if ((i == 0 || second) && ok[i]) {
+      float4 p = pv[i][0];  // partials in split order, then the residual (as split_sum4 + add)
+#pragma unroll
+      for (int sp = 1; sp < SMAX; ++sp)
+        if (sp < splits) {
+          p.x += pv[i][sp].x;
+          p.y += pv[i][sp].y;
+          p.z += pv[i][sp].z;
+          p.w += pv[i][sp].w;
+        }
+      t = make_float4(q[i].x + p.x, q[i].y + p.y, q[i].z + p.z, q[i].w + p.w);
+      *reinterpret_cast<float4*>(h_out + idx[i]) = t;
     }
     v[i] = t;
     ss += t.x * t.x + t.y * t.y + t.z * t.z + t.w * t.w;
   }
-  // The norm weights do not depend on the sum: load them before the reduction.
-  float4 wv[2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int c = 4 * (threadIdx.x + i * kRowThreads);
-    wv[i] = c < N ? load4(w + c) : make_float4(0.f, 0.f, 0.f, 0.f);
-  }
   const float scale = 1.0f / sqrtf(block_sum_1024(ss, scratch) / (float)N + eps);
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
-    const int c = 4 * (threadIdx.x + i * kRowThreads);
-    if (c < N)
-      store4(xn + (size_t)r * N + c, make_float4((v[i].x * scale) * wv[i].x, (v[i].y * scale) * wv[i].y,
-                                                 (v[i].z * scale) * wv[i].z, (v[i].w * scale) * wv[i].w));
+    if ((i == 0 || second) && ok[i])
+      store4(xn + idx[i], make_float4((v[i].x * scale) * wv[i].x, (v[i].y * scale) * wv[i].y,
+                                      (v[i].z * scale) * wv[i].z, (v[i].w * scale) * wv[i].w));
   }
 }
 

@@ -69,8 +69,21 @@ struct QkvIn {
   const int32_t* positions; // [batch]: position of the new token
 };
 
-// Sum over the splits in split order (bitwise as the epilogue kernels sum).
+// Sum over the splits in split order (bitwise as the epilogue kernels sum).  Up to
+// kSumUnroll splits every load is issued before the first add (one memory round trip
+// instead of one per split); indices past `splits` re-read split 0 and are dropped.
+constexpr int kSumUnroll = 8;
 __device__ __forceinline__ float sum_splits(const float* __restrict__ p, int splits, size_t plane, size_t idx) {
+  if (splits <= kSumUnroll) {
+    float t[kSumUnroll];
+#pragma unroll
+    for (int s = 0; s < kSumUnroll; ++s) t[s] = p[(size_t)(s < splits ? s : 0) * plane + idx];
+    float v = t[0];
+#pragma unroll
+    for (int s = 1; s < kSumUnroll; ++s)
+      if (s < splits) v += t[s];
+    return v;
+  }
   float v = p[idx];
   for (int s = 1; s < splits; ++s) v += p[(size_t)s * plane + idx];
   return v;

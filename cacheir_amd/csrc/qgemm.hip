@@ -591,6 +591,241 @@ __global__ __launch_bounds__(256 * KG) void qgemm_xs_kernel(const f16* __restric
   }
 }
 
+// ------------------------------------------------------------------ GEMV -----
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+// Raw buffer resource over [p, p + bytes) (gfx9 descriptor word 3: raw byte-addressed
+// loads, out-of-range lanes read 0).
+__device__ __forceinline__ rsrc_t make_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ uint4 buf16(rsrc_t r, uint32_t voff, uint32_t soff) {
+  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+  return uint4{v.x, v.y, v.z, v.w};
+}
+__device__ __forceinline__ uint2 buf8(rsrc_t r, uint32_t voff, uint32_t soff) {
+  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+  const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0);
+  return uint2{v.x, v.y};
+}
+
+// m <= 8 (qgemv_kernel): a workgroup of W wavefronts owns W*NT row tiles, and each
+// wavefront streams its own NT tiles over the workgroup's k-range (grid.y splits k)
+// with no barrier inside the loop.  The m activation rows of that k-range are staged
+// in LDS once, at the start, while the first weight stages are already in flight;
+// per column that is 2*m bytes of activations against 9*W*NT bytes of weights.
+// The MFMA is the GEMM's 16x16x32 step with activation rows past m repeating row
+// m-1 (those outputs are never stored); only the MR accumulator registers that hold
+// rows < m (rows 4*lg + r, r < MR) are scaled and kept.
+constexpr int kGemvMaxRowQuads = 128;  // m * quads per split; LDS = m * (256 * quads + 16) B
+
+template <int FMT, int NT, int MR, int DW, int W>
+__global__ __launch_bounds__(64 * W) void qgemv_kernel(const f16* __restrict__ x, int ldx,
+                                                     const uint8_t* __restrict__ wq, const uint16_t* __restrict__ wd,
+                                                     float* __restrict__ part, int M, int N, int K, int nq) {
+  constexpr int LB = Stage<FMT, NT, 1>::LB;
+  constexpr int kChunks = 16 * kGemvMaxRowQuads / (64 * W);  // 16-byte activation chunks per thread, at most
+  extern __shared__ __align__(16) uint8_t xs[];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63, li = lane & 15, lg = lane >> 4;
+  const int KQ = K / 128, NTILES = (N + 15) / 16;
+  const int nt0 = (blockIdx.x * W + wave) * NT;
+  const int split = blockIdx.y;
+  const int q0 = split * nq;
+  const int rs = 256 * nq + 16;  // LDS row stride: consecutive rows start 4 banks apart
+
+  // Activation loads first (the load counter retires in order, so the LDS writes
+  // below wait for these and not for the weight stages issued after them).
+  // Chunk c (16 B) = row c / (16 nq), column chunk c % (16 nq); chunks past the end
+  // repeat the last one (same value to the same LDS address).
+  const int cols16 = 16 * nq, total = M * cols16;
+  const int r_step = (64 * W) / cols16, c_step = (64 * W) - r_step * cols16;  // uniform
+  u32x4 xv[kChunks];
+  int xoff[kChunks];
+  {
+    int r = (int)threadIdx.x / cols16, col = (int)threadIdx.x - r * cols16;
+#pragma unroll
+    for (int u = 0; u < kChunks; ++u) {
+      const bool past = r >= M;
+      const int rr = past ? M - 1 : r, cc = past ? cols16 - 1 : col;
+      xv[u] = *reinterpret_cast<const u32x4*>(x + (size_t)rr * ldx + 128 * q0 + 8 * cc);
+      xoff[u] = rr * rs + 16 * cc;
+      r += r_step;
+      col += c_step;
+      if (col >= cols16) col -= cols16, ++r;
+    }
+  }
+
+  // Weight loads go through buffer resources: the tile offset is wavefront-uniform
+  // (an SGPR), the lane offset a fixed VGPR, so no 64-bit address lives in VGPRs.
+  const uint32_t ntiles_total = (uint32_t)NTILES * KQ;
+  const rsrc_t rw = make_rsrc(wq, ntiles_total * 1024u * LB);
+  const rsrc_t rd = make_rsrc(wd, is_row_fmt(FMT) ? 0u : ntiles_total * 128u);
+  uint32_t tb[NT];
+#pragma unroll
+  for (int b = 0; b < NT; ++b) tb[b] = (uint32_t)min(nt0 + b, NTILES - 1) * KQ + q0;
+  const uint32_t vw = (uint32_t)lane * 16u * LB, vd = (uint32_t)li * 8u;
+  struct WS {
+    uint4 w[NT][LB];
+    uint2 d[NT];
+  };
+  // Ring of DW + 1 slots: the stage of quad i loads quad i + DW into the slot that
+  // quad i - 1 has just freed, so no slot holds two live values and the loads go out
+  // before the stage's compute.
+  constexpr int R = DW + 1;
+  WS ws[R];
+  auto issue = [&](int slot, int idx) __attribute__((always_inline)) {  // quad idx, clamped to the last
+    const uint32_t Q = (uint32_t)min(idx, nq - 1);
+#pragma unroll
+    for (int b = 0; b < NT; ++b) {
+#pragma unroll
+      for (int c = 0; c < LB; ++c) ws[slot].w[b][c] = buf16(rw, vw + 16u * c, (tb[b] + Q) * 1024u * LB);
+      if constexpr (!is_row_fmt(FMT)) ws[slot].d[b] = buf8(rd, vd, (tb[b] + Q) * 128u);
+    }
+  };
+  auto each = [&]<int C>(auto&& f) __attribute__((always_inline)) {
+    [&]<int... S>(std::integer_sequence<int, S...>) { (f.template operator()<S>(), ...); }(
+        std::make_integer_sequence<int, C>{});
+  };
+  each.template operator()<DW>([&]<int S>() { issue(S, S); });
+
+#pragma unroll
+  for (int u = 0; u < kChunks; ++u) *reinterpret_cast<u32x4*>(&xs[xoff[u]]) = xv[u];
+  __syncthreads();
+
+  f32x4 acc[NT];
+  f32x4 sx = {0.f, 0.f, 0.f, 0.f};  // row formats: activation sums of this split
+#pragma unroll
+  for (int b = 0; b < NT; ++b) acc[b] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const uint8_t* xrow = xs + min(li, M - 1) * rs + 16 * lg;
+
+  auto compute = [&](const WS& st, int idx) __attribute__((always_inline)) {
+    f16x8 xf[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) xf[j] = *reinterpret_cast<const f16x8*>(xrow + 256 * idx + 64 * j);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      f32x4 c[NT];
+      float dj[NT];
+#pragma unroll
+      for (int b = 0; b < NT; ++b) {
+        f16x8 wb;
+        if constexpr (layout_fmt(FMT) == CIR_Q4_0) {
+          const uint4 v = st.w[b][0];
+          wb = dq_q4((j == 0) ? v.x : (j == 1) ? v.y : (j == 2) ? v.z : v.w);
+        } else {
+          const uint4 v = st.w[b][j >> 1];
+          wb = dq_q8((j & 1) ? v.z : v.x, (j & 1) ? v.w : v.y);
+        }
+        if constexpr (is_row_fmt(FMT)) {
+          acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xf[j], wb, acc[b], 0, 0, 0);
+        } else {
+          const uint32_t dw = (j < 2) ? st.d[b].x : st.d[b].y;
+          dj[b] = static_cast<float>(__builtin_bit_cast(f16, (uint16_t)((j & 1) ? (dw >> 16) : (dw & 0xFFFFu))));
+          c[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xf[j], wb, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+        }
+      }
+      if constexpr (is_row_fmt(FMT)) {
+        const f16x8 ones = {1, 1, 1, 1, 1, 1, 1, 1};
+        sx = __builtin_amdgcn_mfma_f32_16x16x32_f16(xf[j], ones, sx, 0, 0, 0);
+      } else {
+#pragma unroll
+        for (int b = 0; b < NT; ++b) {
+#pragma unroll
+          for (int r = 0; r < MR; ++r) acc[b][r] = fmaf(dj[b], c[b][r], acc[b][r]);
+          // Rows MR..3 are never read.  Without this use the register allocator may hand
+          // their registers to the next dequant's inline v_and_or_b32 while the MFMA that
+          // writes them is still in flight; no wait is inserted for an inline-asm writer,
+          // so the late MFMA write would clobber the next B operand.  The empty statement
+          // reads all four and is ordered after the FMAs (it "updates" acc[b]), whose read
+          // of the result waits for the MFMA to finish.
+          if constexpr (MR < 4) asm volatile("" : "+v"(acc[b]) : "v"(c[b]));
+        }
+      }
+    }
+  };
+
+  int i = 0;
+#pragma nounroll
+  for (; i + R <= nq; i += R) {
+    each.template operator()<R>([&]<int S>() {
+      issue((S + DW) % R, i + S + DW);
+      compute(ws[S], i + S);
+      __builtin_amdgcn_sched_barrier(0);  // keep stages apart: hoisting across them only adds registers
+    });
+  }
+  each.template operator()<DW>([&]<int S>() {  // at most DW quads are left, in slots 0 .. DW-1
+    if (i + S < nq) compute(ws[S], i + S);
+  });
+
+  if constexpr (is_row_fmt(FMT)) {
+    const float* rscale = reinterpret_cast<const float*>(wd);
+    const float* roff = rscale + (size_t)NTILES * 16;
+#pragma unroll
+    for (int b = 0; b < NT; ++b) {
+      const int n = min(nt0 + b, NTILES - 1) * 16 + li;
+      const float sc = rscale[n], of = roff[n];
+#pragma unroll
+      for (int r = 0; r < MR; ++r) acc[b][r] = sc * fmaf(of, sx[r], acc[b][r]);
+    }
+  }
+#pragma unroll
+  for (int b = 0; b < NT; ++b) {
+    const int n = (nt0 + b) * 16 + li;
+    if (nt0 + b < NTILES && n < N) {
+#pragma unroll
+      for (int r = 0; r < MR; ++r) {
+        const int m = 4 * lg + r;
+        if (m < M) part[((size_t)split * M + m) * N + n] = acc[b][r];
+      }
+    }
+  }
+}
+
+#ifndef CIR_GV_W
+#define CIR_GV_W 8
+#endif
+#ifndef CIR_GV_NT
+#define CIR_GV_NT 1
+#endif
+#ifndef CIR_GV_DW
+#define CIR_GV_DW 4
+#endif
+#ifndef CIR_GV_GROUPS
+#define CIR_GV_GROUPS 512
+#endif
+
+constexpr int kGemvRowsPerGroup = 16 * CIR_GV_W * CIR_GV_NT;
+
+bool gemv_fits(int m, int k, int splits) { return m <= 8 && m * ((k / 128) / splits) <= kGemvMaxRowQuads; }
+
+// GEMV k-split: the smallest power of two with m * quads <= kGemvMaxRowQuads that gives
+// >= CIR_GV_GROUPS workgroups, keeping at least 4 quads per split.  0 when no split fits.
+int gemv_splits(int m, int n, int k) {
+  const int kq = k / 128;
+  const long groups = (n + kGemvRowsPerGroup - 1) / kGemvRowsPerGroup;
+  int s = 1;
+  while (m * (kq / s) > kGemvMaxRowQuads && kq % (2 * s) == 0) s *= 2;
+  if (!gemv_fits(m, k, s) || kq % s) return 0;
+  while (groups * s < CIR_GV_GROUPS && kq % (2 * s) == 0 && kq / (2 * s) >= 4) s *= 2;
+  return s;
+}
+
+template <int FMT>
+void launch_qgemv(const f16* x, int ldx, const uint8_t* wq, const uint16_t* wd, float* part, int M, int N, int K,
+                  int splits, hipStream_t s) {
+  const int NTILES = (N + 15) / 16;
+  const int nq = (K / 128) / splits;
+  dim3 grid((NTILES + CIR_GV_W * CIR_GV_NT - 1) / (CIR_GV_W * CIR_GV_NT), splits);
+  const size_t lds = (size_t)M * (256 * nq + 16);
+  auto go = [&]<int MR>() {
+    qgemv_kernel<FMT, CIR_GV_NT, MR, CIR_GV_DW, CIR_GV_W>
+        <<<grid, 64 * CIR_GV_W, lds, s>>>(x, ldx, wq, wd, part, M, N, K, nq);
+  };
+  if (M == 1) go.template operator()<1>();
+  else if (M == 2) go.template operator()<2>();
+  else go.template operator()<4>();
+}
+
 #ifndef CIR_XS_DW
 #define CIR_XS_DW 4
 #endif
@@ -713,6 +948,9 @@ constexpr int xs_rows_per_group(int m) { return m <= 16 ? 64 : 128; }
 // k-split: the smallest power of two that gives >= 192 workgroups, keeping at least
 // 4 quads per split (split-k partials cost 4*m*n bytes each, so no more than needed).
 int default_splits(int m, int n, int k) {
+  if (m <= 8) {
+    if (const int s = gemv_splits(m, n, k)) return s;
+  }
   const int kq = k / 128;
   const long groups = (long)((n + xs_rows_per_group(m) - 1) / xs_rows_per_group(m)) * ((m + 31) / 32);
   int s = 1;
@@ -723,7 +961,8 @@ int default_splits(int m, int n, int k) {
 template <int FMT>
 void dispatch_qgemm(const f16* x, int ldx, const uint8_t* wq, const uint16_t* wd, float* part, int M, int N, int K,
                     int splits, hipStream_t s) {
-  if (M <= 16) launch_qgemm_xs<FMT, 1, 1, 4>(x, ldx, wq, wd, part, M, N, K, splits, s);
+  if (gemv_fits(M, K, splits)) launch_qgemv<FMT>(x, ldx, wq, wd, part, M, N, K, splits, s);
+  else if (M <= 16) launch_qgemm_xs<FMT, 1, 1, 4>(x, ldx, wq, wd, part, M, N, K, splits, s);
   else launch_qgemm_xs<FMT, 2, 2, CIR_XS_DW>(x, ldx, wq, wd, part, M, N, K, splits, s);
 }
 

@@ -181,6 +181,39 @@ def test_qgemm_config3_shapes(device, fmt, n, k, m):
     close16(got, ops.matmul(x.astype(np.float32), wf))
 
 
+@pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
+def test_qgemv_every_small_batch(device, fmt):
+    """Batches of 1..8 rows (the GEMV kernel, whose scaled accumulator registers depend on the row count): every
+    row count, a ragged n, k-splits 1, 2 and 5 of 10 quads (ring tails of every length), and one split too long
+    for the GEMV's activation stage (m * quads > 128, served by the MFMA GEMM). Each split's partials are checked,
+    not only their sum, against the exact-product bound of fp64 and the fp16 bound of the oracle."""
+    from cacheir_amd import kernels
+
+    rng = np.random.default_rng(4242)
+    n, k = 200, 1280
+    enc, dec = (quant.random_q4_0, quant.decode_q4_0) if fmt == "q4_0" else (quant.random_q8_0, quant.decode_q8_0)
+    blocks = enc(rng, n, k)[0]
+    wf = dec(blocks, k).astype(np.float64)
+    w = kernels.QWeight.from_blocks(to_dev(blocks.reshape(-1), device), kernels.FMT_NAMES[fmt], n, k)
+    for m in range(1, 9):
+        x = rng.standard_normal((m, k)).astype(np.float16)
+        xd = to_dev(x, device)
+        for splits in (1, 2, 5):
+            part = kernels.qgemm_partial(xd, w, splits=splits).double().cpu().numpy()
+            kq = k // 128 // splits
+            for s in range(splits):
+                xs = x[:, s * kq * 128:(s + 1) * kq * 128].astype(np.float64)
+                ws_ = wf[:, s * kq * 128:(s + 1) * kq * 128]
+                bound = 1e-5 * (np.abs(xs) @ np.abs(ws_).T) + 1e-6
+                assert np.all(np.abs(part[s] - xs @ ws_.T) <= bound), (m, splits, s)
+            close16(part.sum(0), ops.matmul(x.astype(np.float32), wf.astype(np.float32)))
+    x = rng.standard_normal((8, 4096)).astype(np.float16)
+    blocks = enc(rng, 48, 4096)[0]
+    w = kernels.QWeight.from_blocks(to_dev(blocks.reshape(-1), device), kernels.FMT_NAMES[fmt], 48, 4096)
+    got = kernels.qgemm_partial(to_dev(x, device), w, splits=1)[0].cpu().numpy()
+    close16(got, ops.matmul(x.astype(np.float32), dec(blocks, 4096)))
+
+
 def test_gemm_f32(device):
     from cacheir_amd import kernels
 

@@ -617,18 +617,27 @@ __device__ __forceinline__ uint2 buf8(rsrc_t r, uint32_t voff, uint32_t soff) {
 // m-1 (those outputs are never stored); only the MR accumulator registers that hold
 // rows < m (rows 4*lg + r, r < MR) are scaled and kept.
 constexpr int kGemvMaxRowQuads = 128;  // m * quads per split; LDS = m * (256 * quads + 16) B
+constexpr int kGemvMaxWaves = 16;
 
-template <int FMT, int NT, int MR, int DW, int W>
-__global__ __launch_bounds__(64 * W) void qgemv_kernel(const f16* __restrict__ x, int ldx,
-                                                     const uint8_t* __restrict__ wq, const uint16_t* __restrict__ wd,
-                                                     float* __restrict__ part, int M, int N, int K, int nq) {
-  constexpr int LB = Stage<FMT, NT, 1>::LB;
-  constexpr int kChunks = 16 * kGemvMaxRowQuads / (64 * W);  // 16-byte activation chunks per thread, at most
+// Workgroup = blockDim.x / 64 wavefronts (runtime); wavefront v of workgroup g in
+// split s owns tiles (g * W + v) * tpw .. + tpw - 1 and streams them one after the
+// other, each over the split's nq quads: tpw * nq ring stages with no drain between
+// tiles.  A finished tile's accumulators go to part[s][m][n] and restart at zero.
+// XC: 16-byte activation chunks per thread (the host makes XC * blockDim.x cover
+// the m * 16 * nq chunks of the split).
+template <int FMT, int MR, int DW, int XC>
+__global__ __launch_bounds__(64 * kGemvMaxWaves) void qgemv_kernel(const f16* __restrict__ x, int ldx,
+                                                                 const uint8_t* __restrict__ wq,
+                                                                 const uint16_t* __restrict__ wd,
+                                                                 float* __restrict__ part, int M, int N, int K,
+                                                                 int nq, int tpw) {
+  constexpr int LB = Stage<FMT, 1, 1>::LB;
   extern __shared__ __align__(16) uint8_t xs[];
+  const int W = __builtin_amdgcn_readfirstlane(blockDim.x >> 6);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63, li = lane & 15, lg = lane >> 4;
   const int KQ = K / 128, NTILES = (N + 15) / 16;
-  const int nt0 = (blockIdx.x * W + wave) * NT;
+  const int t0 = (blockIdx.x * W + wave) * tpw;  // this wavefront's first tile
   const int split = blockIdx.y;
   const int q0 = split * nq;
   const int rs = 256 * nq + 16;  // LDS row stride: consecutive rows start 4 banks apart
@@ -637,14 +646,15 @@ __global__ __launch_bounds__(64 * W) void qgemv_kernel(const f16* __restrict__ x
   // below wait for these and not for the weight stages issued after them).
   // Chunk c (16 B) = row c / (16 nq), column chunk c % (16 nq); chunks past the end
   // repeat the last one (same value to the same LDS address).
-  const int cols16 = 16 * nq, total = M * cols16;
-  const int r_step = (64 * W) / cols16, c_step = (64 * W) - r_step * cols16;  // uniform
-  u32x4 xv[kChunks];
-  int xoff[kChunks];
+  const int nthr = 64 * W;
+  const int cols16 = 16 * nq;
+  const int r_step = nthr / cols16, c_step = nthr - r_step * cols16;  // uniform
+  u32x4 xv[XC];
+  int xoff[XC];
   {
     int r = (int)threadIdx.x / cols16, col = (int)threadIdx.x - r * cols16;
 #pragma unroll
-    for (int u = 0; u < kChunks; ++u) {
+    for (int u = 0; u < XC; ++u) {
       const bool past = r >= M;
       const int rr = past ? M - 1 : r, cc = past ? cols16 - 1 : col;
       xv[u] = *reinterpret_cast<const u32x4*>(x + (size_t)rr * ldx + 128 * q0 + 8 * cc);
@@ -660,154 +670,176 @@ __global__ __launch_bounds__(64 * W) void qgemv_kernel(const f16* __restrict__ x
   const uint32_t ntiles_total = (uint32_t)NTILES * KQ;
   const rsrc_t rw = make_rsrc(wq, ntiles_total * 1024u * LB);
   const rsrc_t rd = make_rsrc(wd, is_row_fmt(FMT) ? 0u : ntiles_total * 128u);
-  uint32_t tb[NT];
-#pragma unroll
-  for (int b = 0; b < NT; ++b) tb[b] = (uint32_t)min(nt0 + b, NTILES - 1) * KQ + q0;
   const uint32_t vw = (uint32_t)lane * 16u * LB, vd = (uint32_t)li * 8u;
   struct WS {
-    uint4 w[NT][LB];
-    uint2 d[NT];
+    uint4 w[LB];
+    uint2 d;
   };
-  // Ring of DW + 1 slots: the stage of quad i loads quad i + DW into the slot that
-  // quad i - 1 has just freed, so no slot holds two live values and the loads go out
+  // Ring of DW + 1 slots: the stage of quad i loads stage i + DW into the slot that
+  // stage i - 1 has just freed, so no slot holds two live values and the loads go out
   // before the stage's compute.
   constexpr int R = DW + 1;
   WS ws[R];
-  auto issue = [&](int slot, int idx) __attribute__((always_inline)) {  // quad idx, clamped to the last
-    const uint32_t Q = (uint32_t)min(idx, nq - 1);
+  int il = 0, iq = 0;  // next stage to load: tile il of the wavefront, quad iq of the split
+  auto issue = [&](int slot) __attribute__((always_inline)) {  // past the last stage: reload the last
+    const bool past = il >= tpw;
+    const uint32_t tb = (uint32_t)min(t0 + (past ? tpw - 1 : il), NTILES - 1) * KQ + q0 + (past ? nq - 1 : iq);
 #pragma unroll
-    for (int b = 0; b < NT; ++b) {
-#pragma unroll
-      for (int c = 0; c < LB; ++c) ws[slot].w[b][c] = buf16(rw, vw + 16u * c, (tb[b] + Q) * 1024u * LB);
-      if constexpr (!is_row_fmt(FMT)) ws[slot].d[b] = buf8(rd, vd, (tb[b] + Q) * 128u);
-    }
+    for (int c = 0; c < LB; ++c) ws[slot].w[c] = buf16(rw, vw + 16u * c, tb * 1024u * LB);
+    if constexpr (!is_row_fmt(FMT)) ws[slot].d = buf8(rd, vd, tb * 128u);
+    if (++iq == nq) iq = 0, ++il;
   };
   auto each = [&]<int C>(auto&& f) __attribute__((always_inline)) {
     [&]<int... S>(std::integer_sequence<int, S...>) { (f.template operator()<S>(), ...); }(
         std::make_integer_sequence<int, C>{});
   };
-  each.template operator()<DW>([&]<int S>() { issue(S, S); });
+  each.template operator()<DW>([&]<int S>() { issue(S); });
 
 #pragma unroll
-  for (int u = 0; u < kChunks; ++u) *reinterpret_cast<u32x4*>(&xs[xoff[u]]) = xv[u];
+  for (int u = 0; u < XC; ++u) *reinterpret_cast<u32x4*>(&xs[xoff[u]]) = xv[u];
   __syncthreads();
 
-  f32x4 acc[NT];
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   f32x4 sx = {0.f, 0.f, 0.f, 0.f};  // row formats: activation sums of this split
-#pragma unroll
-  for (int b = 0; b < NT; ++b) acc[b] = f32x4{0.f, 0.f, 0.f, 0.f};
   const uint8_t* xrow = xs + min(li, M - 1) * rs + 16 * lg;
+  int cl = 0, cq = 0;  // stage being computed
 
-  auto compute = [&](const WS& st, int idx) __attribute__((always_inline)) {
-    f16x8 xf[4];
+  // Rows past m hold MFMA results nobody reads; acc rows are 4 * lg + r.
+  auto store_tile = [&]() __attribute__((always_inline)) {
+    const int t = t0 + cl;
+    const int n = t * 16 + li;
+    if constexpr (is_row_fmt(FMT)) {
+      // w = (c - zp) * s with c the stored code: acc holds sum x*c over this split,
+      // so the split's share of y is s * (acc + (c0 - zp) * sum x), c0 - zp = offset[row].
+      const float* rscale = reinterpret_cast<const float*>(wd);
+      const float* roff = rscale + (size_t)NTILES * 16;
+      const int nn = min(t, NTILES - 1) * 16 + li;
+      const float sc = rscale[nn], of = roff[nn];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) xf[j] = *reinterpret_cast<const f16x8*>(xrow + 256 * idx + 64 * j);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      f32x4 c[NT];
-      float dj[NT];
-#pragma unroll
-      for (int b = 0; b < NT; ++b) {
-        f16x8 wb;
-        if constexpr (layout_fmt(FMT) == CIR_Q4_0) {
-          const uint4 v = st.w[b][0];
-          wb = dq_q4((j == 0) ? v.x : (j == 1) ? v.y : (j == 2) ? v.z : v.w);
-        } else {
-          const uint4 v = st.w[b][j >> 1];
-          wb = dq_q8((j & 1) ? v.z : v.x, (j & 1) ? v.w : v.y);
-        }
-        if constexpr (is_row_fmt(FMT)) {
-          acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xf[j], wb, acc[b], 0, 0, 0);
-        } else {
-          const uint32_t dw = (j < 2) ? st.d[b].x : st.d[b].y;
-          dj[b] = static_cast<float>(__builtin_bit_cast(f16, (uint16_t)((j & 1) ? (dw >> 16) : (dw & 0xFFFFu))));
-          c[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xf[j], wb, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-        }
-      }
-      if constexpr (is_row_fmt(FMT)) {
-        const f16x8 ones = {1, 1, 1, 1, 1, 1, 1, 1};
-        sx = __builtin_amdgcn_mfma_f32_16x16x32_f16(xf[j], ones, sx, 0, 0, 0);
-      } else {
-#pragma unroll
-        for (int b = 0; b < NT; ++b) {
-#pragma unroll
-          for (int r = 0; r < MR; ++r) acc[b][r] = fmaf(dj[b], c[b][r], acc[b][r]);
-          // Rows MR..3 are never read.  Without this use the register allocator may hand
-          // their registers to the next dequant's inline v_and_or_b32 while the MFMA that
-          // writes them is still in flight; no wait is inserted for an inline-asm writer,
-          // so the late MFMA write would clobber the next B operand.  The empty statement
-          // reads all four and is ordered after the FMAs (it "updates" acc[b]), whose read
-          // of the result waits for the MFMA to finish.
-          if constexpr (MR < 4) asm volatile("" : "+v"(acc[b]) : "v"(c[b]));
-        }
-      }
+      for (int r = 0; r < MR; ++r) acc[r] = sc * fmaf(of, sx[r], acc[r]);
     }
-  };
-
-  int i = 0;
-#pragma nounroll
-  for (; i + R <= nq; i += R) {
-    each.template operator()<R>([&]<int S>() {
-      issue((S + DW) % R, i + S + DW);
-      compute(ws[S], i + S);
-      __builtin_amdgcn_sched_barrier(0);  // keep stages apart: hoisting across them only adds registers
-    });
-  }
-  each.template operator()<DW>([&]<int S>() {  // at most DW quads are left, in slots 0 .. DW-1
-    if (i + S < nq) compute(ws[S], i + S);
-  });
-
-  if constexpr (is_row_fmt(FMT)) {
-    const float* rscale = reinterpret_cast<const float*>(wd);
-    const float* roff = rscale + (size_t)NTILES * 16;
-#pragma unroll
-    for (int b = 0; b < NT; ++b) {
-      const int n = min(nt0 + b, NTILES - 1) * 16 + li;
-      const float sc = rscale[n], of = roff[n];
-#pragma unroll
-      for (int r = 0; r < MR; ++r) acc[b][r] = sc * fmaf(of, sx[r], acc[b][r]);
-    }
-  }
-#pragma unroll
-  for (int b = 0; b < NT; ++b) {
-    const int n = (nt0 + b) * 16 + li;
-    if (nt0 + b < NTILES && n < N) {
+    if (t < NTILES && n < N) {
 #pragma unroll
       for (int r = 0; r < MR; ++r) {
         const int m = 4 * lg + r;
-        if (m < M) part[((size_t)split * M + m) * N + n] = acc[b][r];
+        if (m < M) part[((size_t)split * M + m) * N + n] = acc[r];
       }
     }
+    acc = f32x4{0.f, 0.f, 0.f, 0.f};
+    sx = f32x4{0.f, 0.f, 0.f, 0.f};
+  };
+
+  auto compute = [&](const WS& st) __attribute__((always_inline)) {
+    f16x8 xf[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) xf[j] = *reinterpret_cast<const f16x8*>(xrow + 256 * cq + 64 * j);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      f16x8 wb;
+      if constexpr (layout_fmt(FMT) == CIR_Q4_0) {
+        const uint4 v = st.w[0];
+        wb = dq_q4((j == 0) ? v.x : (j == 1) ? v.y : (j == 2) ? v.z : v.w);
+      } else {
+        const uint4 v = st.w[j >> 1];
+        wb = dq_q8((j & 1) ? v.z : v.x, (j & 1) ? v.w : v.y);
+      }
+      if constexpr (is_row_fmt(FMT)) {
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xf[j], wb, acc, 0, 0, 0);
+        const f16x8 ones = {1, 1, 1, 1, 1, 1, 1, 1};
+        sx = __builtin_amdgcn_mfma_f32_16x16x32_f16(xf[j], ones, sx, 0, 0, 0);
+      } else {
+        const uint32_t dw = (j < 2) ? st.d.x : st.d.y;
+        const float dj = static_cast<float>(__builtin_bit_cast(f16, (uint16_t)((j & 1) ? (dw >> 16) : (dw & 0xFFFFu))));
+        const f32x4 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(xf[j], wb, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < MR; ++r) acc[r] = fmaf(dj, c[r], acc[r]);
+        // Rows MR..3 of c are never read.  Without this use the register allocator may
+        // hand their registers to the next dequant's inline v_and_or_b32 while the MFMA
+        // that writes them is still in flight; no wait is inserted for an inline-asm
+        // writer, so the late MFMA write would clobber the next B operand.  The empty
+        // statement reads all four and is ordered after the FMAs (it "updates" acc),
+        // whose read of the result waits for the MFMA to finish.
+        if constexpr (MR < 4) asm volatile("" : "+v"(acc) : "v"(c));
+      }
+    }
+    if (cq == nq - 1) store_tile();  // uniform
+    if (++cq == nq) cq = 0, ++cl;
+  };
+
+  const int T = tpw * nq;
+  int i = 0;
+#pragma nounroll
+  for (; i + R <= T; i += R) {
+    each.template operator()<R>([&]<int S>() {
+      issue((S + DW) % R);
+      compute(ws[S]);
+      __builtin_amdgcn_sched_barrier(0);  // keep stages apart: hoisting across them only adds registers
+    });
   }
+  each.template operator()<DW>([&]<int S>() {  // at most DW stages are left, in slots 0 .. DW-1
+    if (i + S < T) compute(ws[S]);
+  });
 }
 
-#ifndef CIR_GV_W
-#define CIR_GV_W 8
-#endif
-#ifndef CIR_GV_NT
-#define CIR_GV_NT 1
-#endif
 #ifndef CIR_GV_DW
 #define CIR_GV_DW 4
 #endif
-#ifndef CIR_GV_GROUPS
-#define CIR_GV_GROUPS 512
-#endif
-
-constexpr int kGemvRowsPerGroup = 16 * CIR_GV_W * CIR_GV_NT;
 
 bool gemv_fits(int m, int k, int splits) { return m <= 8 && m * ((k / 128) / splits) <= kGemvMaxRowQuads; }
 
-// GEMV k-split: the smallest power of two with m * quads <= kGemvMaxRowQuads that gives
-// >= CIR_GV_GROUPS workgroups, keeping at least 4 quads per split.  0 when no split fits.
+// GEMV launch geometry for a given split: W wavefronts per workgroup and tpw tiles per
+// wavefront.  Every workgroup should be resident at once and every CU should stream
+// the same number of tile-quads, since a CU's share of HBM bandwidth is bounded (its
+// L1 miss queue): the busiest CU sets the time.  Measured on MI355X at the Llama-3-8B
+// shapes: 6-8 wavefronts per CU stream best (4 leave the miss queue short, 14-16
+// lose 1-4 us), and the number of tiles per wavefront hardly matters.  So W is 6..8
+// and, among those, take the least busiest-CU work, then the fewest workgroups (each
+// stages its activations once).
+struct GemvGeom {
+  int waves, tpw;
+};
+constexpr int kCUs = 256;
+GemvGeom gemv_geometry(int m, int n, int k, int splits) {
+  const int ntiles = (n + 15) / 16, nq = (k / 128) / splits;
+  const size_t lds = (size_t)m * (256 * nq + 16);
+  GemvGeom best{8, 1};
+  long best_work = -1, best_groups = 0;
+  for (int w = 6; w <= 8; ++w) {
+    const int by_lds = (int)(160 * 1024 / lds);
+    const int per_cu_cap = min(32 / w, by_lds);  // resident workgroups per CU (8 wavefronts per SIMD)
+    if (per_cu_cap < 1) continue;
+    for (int tpw = 1; tpw <= 64; ++tpw) {
+      const long groups = (long)splits * ((ntiles + w * tpw - 1) / (w * tpw));
+      const long per_cu = (groups + kCUs - 1) / kCUs;
+      if (per_cu > per_cu_cap) continue;
+      const long work = per_cu * w * tpw * nq;
+      if (best_work < 0 || work < best_work || (work == best_work && groups < best_groups)) {
+        best = GemvGeom{w, tpw};
+        best_work = work;
+        best_groups = groups;
+      }
+    }
+  }
+  return best;
+}
+
+// GEMV k-split: over powers of two with m * quads <= kGemvMaxRowQuads, the least
+// estimated time: busiest-CU weight bytes at 7 TB/s / 256 plus the partials written
+// and read back by the epilogue (8 * splits * m * n bytes at 7 TB/s).  0: none fits.
 int gemv_splits(int m, int n, int k) {
   const int kq = k / 128;
-  const long groups = (n + kGemvRowsPerGroup - 1) / kGemvRowsPerGroup;
-  int s = 1;
-  while (m * (kq / s) > kGemvMaxRowQuads && kq % (2 * s) == 0) s *= 2;
-  if (!gemv_fits(m, k, s) || kq % s) return 0;
-  while (groups * s < CIR_GV_GROUPS && kq % (2 * s) == 0 && kq / (2 * s) >= 4) s *= 2;
-  return s;
+  int best = 0;
+  double best_t = 0;
+  for (int s = 1; s <= kq && s <= 64; s *= 2) {
+    if (kq % s || !gemv_fits(m, k, s)) continue;
+    const GemvGeom g = gemv_geometry(m, n, k, s);
+    const int ntiles = (n + 15) / 16, nq = kq / s;
+    const long groups = (long)s * ((ntiles + g.waves * g.tpw - 1) / (g.waves * g.tpw));
+    const long per_cu = (groups + kCUs - 1) / kCUs;
+    const double t = per_cu * g.waves * g.tpw * nq * 1152.0 / (7e12 / kCUs) + 8.0 * s * m * n / 7e12;
+    if (!best || t < best_t) best = s, best_t = t;
+  }
+  return best;
 }
 
 template <int FMT>
@@ -815,15 +847,30 @@ void launch_qgemv(const f16* x, int ldx, const uint8_t* wq, const uint16_t* wd, 
                   int splits, hipStream_t s) {
   const int NTILES = (N + 15) / 16;
   const int nq = (K / 128) / splits;
-  dim3 grid((NTILES + CIR_GV_W * CIR_GV_NT - 1) / (CIR_GV_W * CIR_GV_NT), splits);
+  GemvGeom g = gemv_geometry(M, N, K, splits);
+  if constexpr (is_row_fmt(FMT)) g.tpw = 1;  // the row scales are read once, after the loop
+  const int waves_per_split = (NTILES + g.tpw - 1) / g.tpw;
+  dim3 grid((waves_per_split + g.waves - 1) / g.waves, splits);
   const size_t lds = (size_t)M * (256 * nq + 16);
-  auto go = [&]<int MR>() {
-    qgemv_kernel<FMT, CIR_GV_NT, MR, CIR_GV_DW, CIR_GV_W>
-        <<<grid, 64 * CIR_GV_W, lds, s>>>(x, ldx, wq, wd, part, M, N, K, nq);
+  const int xc_need = (16 * M * nq + 64 * g.waves - 1) / (64 * g.waves);
+  auto go = [&]<int MR, int XC>() {
+    qgemv_kernel<FMT, MR, CIR_GV_DW, XC><<<grid, 64 * g.waves, lds, s>>>(x, ldx, wq, wd, part, M, N, K, nq, g.tpw);
   };
-  if (M == 1) go.template operator()<1>();
-  else if (M == 2) go.template operator()<2>();
-  else go.template operator()<4>();
+  auto by_xc = [&]<int MR>() {
+    if (xc_need <= 1) go.template operator()<MR, 1>();
+    else if (xc_need <= 2) go.template operator()<MR, 2>();
+    else if (xc_need <= 4) go.template operator()<MR, 4>();
+    else go.template operator()<MR, 8>();
+  };
+  // Row formats keep all four accumulator rows: their MFMA chains carry every row to
+  // the final scale, which reads them all (no row's registers are freed early).
+  if constexpr (is_row_fmt(FMT)) {
+    by_xc.template operator()<4>();
+  } else {
+    if (M == 1) by_xc.template operator()<1>();
+    else if (M == 2) by_xc.template operator()<2>();
+    else by_xc.template operator()<4>();
+  }
 }
 
 #ifndef CIR_XS_DW

@@ -21,7 +21,8 @@ paged-attention roofline (algorithmic bytes / live HIP-event time of the attenti
 kernel, launches captured in a HIP graph so no host gap is timed, rotated over the 32
 layers' KV so the 256 MB MALL cannot hold it), the same for the largest projection (the
 fused gate|up Q4_0 GEMM + SwiGLU at m = batch, rotated
-over the 32 layers' weights), and a CPU baseline (the C/OpenMP oracle restatement timed on this
+over the 32 layers' weights), the same for the dequant GEMV at m = 1 and 8 (BASELINE
+config 3's 14336 -> 4096 projection, rotated over the layers' down weights), and a CPU baseline (the C/OpenMP oracle restatement timed on this
 host over one layer and the lm_head, scaled to a full step).
 
 roofline.traffic is the HBM bytes per attention launch measured by rocprofv3
@@ -236,6 +237,21 @@ def main() -> int:
     gemm_gbs = gemm_bytes / (gemm_us * 1e-6) / 1e9
     log(f"gate|up GEMM + SwiGLU {gemm_us:.2f} us/launch (m={B}), {gemm_gbs:.0f} GB/s")
 
+    # ---- the dequant GEMV (m <= 8): BASELINE config 3's 14336 -> 4096 projection, on the layers' down weights ----
+    dn = [base.weights.matmul_weight((f"layer{i}_down_w",)) for i in range(cfg.num_layers)]
+    gemv = []
+    for m in (1, 8):
+        xv = torch.randn((m, dn[0].k), device=dev, dtype=torch.float16)
+        sp = kernels.choose_splits(m, dn[0].n, dn[0].k)
+        pv = torch.empty((sp, m, dn[0].n), device=dev)
+        us = graph_us_per_launch(lambda it: kernels.qgemm_partial(xv, dn[it % len(dn)], splits=sp, out=pv),
+                                 args.gemm_iters)
+        by = dn[0].nbytes + 2 * m * dn[0].k + 4 * m * dn[0].n  # weights, x, y once
+        gbs = by / (us * 1e-6) / 1e9
+        gemv.append({"m": m, "n": dn[0].n, "k": dn[0].k, "splits": sp, "us_per_launch": round(us, 3),
+                     "bytes_per_launch": by, "achieved": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)})
+        log(f"GEMV m={m} {dn[0].n}x{dn[0].k} {us:.2f} us/launch, {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%} of peak)")
+
     traffic = measured_traffic(TRAFFIC_FILE)
 
     # ---- CPU baseline: C/OpenMP restatement, one layer + lm_head, scaled to the step ----
@@ -275,6 +291,8 @@ def main() -> int:
                           "achieved": round(gemm_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                           "frac": round(gemm_gbs / HBM_PEAK_GBS, 4), "bytes_per_launch": gemm_bytes,
                           "us_per_launch": round(gemm_us, 3)},
+        "roofline_gemv": {"bound": "hbm", "kernel": "Q4_0 dequant GEMV (qgemv_kernel), BASELINE config 3 down shape",
+                          "peak": HBM_PEAK_GBS, "unit": "GB/s", "shapes": gemv},
         "step_bytes": {"weights": weight_bytes, "kv": kv_bytes * cfg.num_layers,
                        "hbm_floor_ms": round((weight_bytes + kv_bytes * cfg.num_layers) / HBM_PEAK_GBS / 1e6, 4)},
         "cpu_baseline": cpu,

@@ -117,8 +117,9 @@ int cir_qweight_repack_rows(const void* packed, const float* scales, const int32
 int cir_dequant(const void* weights, int tiled, int fmt, float* out, int n, int k, void* stream);
 
 /* The k-split cir_qgemm is tuned for at this shape (a power of two dividing k/128):
- * enough workgroups to fill the GPU, no more partials than that needs.  0 for an
- * invalid shape.  (The reference has no k-split; this replaces its GEMM plan choice,
+ * enough workgroups to fill the GPU, no more partials than that needs (for m <= 8,
+ * the split under which the GEMV gives every CU the same share of the weights).
+ * 0 for an invalid shape.  (The reference has no k-split; this replaces its GEMM plan choice,
  * cacheir/runtime/cuda.py:956-974 _select_gemm_plan.) */
 int cir_qgemm_splits(int m, int n, int k);
 size_t cir_qgemm_workspace_bytes(int m, int n, int splits);
@@ -128,6 +129,9 @@ size_t cir_qgemm_workspace_bytes(int m, int n, int splits);
  * The MFMA multiplies the exact integers (q-8) (Q4_0) or q (Q8_0) in fp16 with x;
  * each 32-value block's fp32 result is scaled by its d in fp32 (exact products:
  * only summation order differs from the fp32 dequant-then-matmul).  fp32 accumulate.
+ * m <= 8 with m * (k/128/splits) <= 128 runs the dequant GEMV (activations staged in
+ * LDS once per workgroup, each wavefront streaming whole tiles); larger m the MFMA
+ * GEMM.  For the same split both give the same partials bit for bit.
  * splits must divide k/128.  Requires k % 128 == 0. */
 int cir_qgemm(const void* x, int ldx, const void* w_tiled, int fmt, float* y_partial,
               int m, int n, int k, int splits, void* stream);

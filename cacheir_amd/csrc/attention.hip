@@ -16,7 +16,9 @@
 //     rows, B = a 16-token tile of K read straight from its page (token rows of
 //     256 B); fp32 accumulate;
 //   * softmax in base 2 (scale*log2(e) folded into the scores): exact within the
-//     block, online (running max / rescale) across a wavefront's blocks;
+//     block, online (running max / rescale) across a wavefront's blocks; the row
+//     max over a tile's 16 token lanes is a DPP reduction (no LDS round trips) and
+//     the rescale factors are read out of their lane as scalars;
 //   * O = P V on VALU: a lane owns 8 contiguous head dims of 4 token rows of each
 //     tile (1 KiB contiguous per load instruction); P comes from the score lanes by
 //     ds_bpermute shuffles; the four token groups are summed once at the end;
@@ -34,6 +36,46 @@
 
 namespace cir {
 namespace {
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+// Max over the 16 lanes of each DPP row (lanes 16r .. 16r+15): swap neighbours, swap
+// pairs, mirror the half rows, mirror the rows; every lane ends with its row's max.
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp_mov<0xB1>(v));   // quad_perm [1,0,3,2]
+  v = fmaxf(v, dpp_mov<0x4E>(v));   // quad_perm [2,3,0,1]
+  v = fmaxf(v, dpp_mov<0x141>(v));  // row_half_mirror
+  v = fmaxf(v, dpp_mov<0x140>(v));  // row_mirror
+  return v;
+}
+// The same pattern as a sum: lane 16r of each row ends with the row's total (the
+// other lanes too, summed in another order).
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp_mov<0xB1>(v);
+  v += dpp_mov<0x4E>(v);
+  v += dpp_mov<0x141>(v);
+  v += dpp_mov<0x140>(v);
+  return v;
+}
+// Sums over the four rows of four values at once, by gfx950's lane-swap instructions
+// (no LDS): v_permlane16_swap(a, b) leaves rows (a0, b0, a2, b2) and (a1, b1, a3, b3),
+// v_permlane32_swap(x, y) leaves (x0, x1, y0, y1) and (x2, x3, y2, y3).  Row k of the
+// result holds the total of v[k], summed (r0 + r1) + (r2 + r3) in every lane.
+__device__ __forceinline__ float swap_sum16(float a, float b) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b),
+                                                  false, false);
+  const uint32_t r0 = r[0], r1 = r[1];  // (bit_cast of a vector element lvalue reads element 0)
+  return __builtin_bit_cast(float, r0) + __builtin_bit_cast(float, r1);
+}
+__device__ __forceinline__ float rows_sum4(const float (&v)[4]) {
+  const float ab = swap_sum16(v[0], v[1]), cd = swap_sum16(v[2], v[3]);
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, ab), __builtin_bit_cast(uint32_t, cd),
+                                                  false, false);
+  const uint32_t r0 = r[0], r1 = r[1];
+  return __builtin_bit_cast(float, r0) + __builtin_bit_cast(float, r1);
+}
 
 // 8 wavefronts of 32-token steps measured best on MI355X at config 4 (batch 32,
 // 2048 tokens), against 64-token steps, 16 wavefronts of 16 tokens and a
@@ -269,8 +311,7 @@ __global__ __launch_bounds__(64 * kWaves) void attn_f16_d128(
       float bm = sc[0][r];
 #pragma unroll
       for (int j = 1; j < kTiles; ++j) bm = fmaxf(bm, sc[j][r]);
-#pragma unroll
-      for (int off = 1; off < 16; off <<= 1) bm = fmaxf(bm, __shfl_xor(bm, off, 64));
+      bm = row16_max(bm);
       const float mn = fmaxf(m[r], bm);  // finite: token tb is always visible
       alpha[r] = exp2f(m[r] - mn);
       float ps = 0.f;
@@ -286,7 +327,8 @@ __global__ __launch_bounds__(64 * kWaves) void attn_f16_d128(
     // Rescale O, then O += P V.  Head h's alpha / p live in lanes 16*(h/4).., register h%4.
 #pragma unroll
     for (int h = 0; h < G; ++h) {
-      const float a = __shfl(alpha[h & 3], 16 * (h >> 2), 64);
+      const float a = __builtin_bit_cast(
+          float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, alpha[h & 3]), 16 * (h >> 2)));  // uniform
 #pragma unroll
       for (int e = 0; e < 8; ++e) acc[h][e] *= a;
     }
@@ -331,20 +373,17 @@ __global__ __launch_bounds__(64 * kWaves) void attn_f16_d128(
     }
   }
 
-  // Wavefront totals: O over the 4 token groups, l over the 16 lanes of a row.
+  // Wavefront totals: O over the 4 token groups (row k of each 4-value sum holds
+  // acc[h][4 * half + k], so every lane writes one), l over the 16 lanes of a row.
 #pragma unroll
   for (int h = 0; h < G; ++h)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      float v = acc[h][e];
-      v += __shfl_xor(v, 16, 64);
-      v += __shfl_xor(v, 32, 64);
-      acc[h][e] = v;
+    for (int half = 0; half < 2; ++half) {
+      const float v[4] = {acc[h][4 * half], acc[h][4 * half + 1], acc[h][4 * half + 2], acc[h][4 * half + 3]};
+      sm_o[wave][h][8 * li + 4 * half + lg] = rows_sum4(v);
     }
 #pragma unroll
-  for (int r = 0; r < 4; ++r)
-#pragma unroll
-    for (int off = 1; off < 16; off <<= 1) lsum[r] += __shfl_xor(lsum[r], off, 64);
+  for (int r = 0; r < 4; ++r) lsum[r] = row16_sum(lsum[r]);
 
   if (li == 0) {
 #pragma unroll
@@ -352,12 +391,6 @@ __global__ __launch_bounds__(64 * kWaves) void attn_f16_d128(
       sm_m[wave][4 * lg + r] = m[r];
       sm_l[wave][4 * lg + r] = lsum[r];
     }
-  }
-  if (lg == 0) {
-#pragma unroll
-    for (int h = 0; h < G; ++h)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) sm_o[wave][h][8 * li + e] = acc[h][e];
   }
   __syncthreads();
 

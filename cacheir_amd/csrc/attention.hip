@@ -21,7 +21,8 @@
 //     the rescale factors are read out of their lane as scalars;
 //   * O = P V on VALU: a lane owns 8 contiguous head dims of 4 token rows of each
 //     tile (1 KiB contiguous per load instruction); P comes from the score lanes by
-//     ds_bpermute shuffles; the four token groups are summed once at the end;
+//     ds_bpermute shuffles, in fp16 with two heads per dword (l sums the same
+//     rounded values); the four token groups are summed once at the end;
 //   * the 8 wavefronts merge (max, sum, O) through LDS with log-sum-exp weights.
 // fp32 pools and other head sizes (tiny-model parity path) use a plain VALU kernel
 // over 128-token chunks that always writes partials, merged by the same kernel.
@@ -317,13 +318,23 @@ __global__ __launch_bounds__(64 * kWaves) void attn_f16_d128(
       float ps = 0.f;
 #pragma unroll
       for (int j = 0; j < kTiles; ++j) {
-        const float p = exp2f(sc[j][r] - mn);
+        // P V takes p in fp16 (two heads per shuffled dword); l sums the same rounded p.
+        const float p = static_cast<float>(static_cast<f16>(exp2f(sc[j][r] - mn)));
         sc[j][r] = p;
         ps += p;
       }
       lsum[r] = lsum[r] * alpha[r] + ps;
       m[r] = mn;
     }
+    // fp16 p of heads (4g, 4g+1) and (4g+2, 4g+3), g = lane / 16, packed for the shuffles.
+    uint32_t pk[kTiles][2];
+#pragma unroll
+    for (int j = 0; j < kTiles; ++j)
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const f16x2 two = {static_cast<f16>(sc[j][2 * q]), static_cast<f16>(sc[j][2 * q + 1])};
+        pk[j][q] = __builtin_bit_cast(uint32_t, two);
+      }
     // Rescale O, then O += P V.  Head h's alpha / p live in lanes 16*(h/4).., register h%4.
 #pragma unroll
     for (int h = 0; h < G; ++h) {
@@ -341,10 +352,16 @@ __global__ __launch_bounds__(64 * kWaves) void attn_f16_d128(
 #pragma unroll
         for (int e = 0; e < 8; ++e) vf[e] = static_cast<float>(o.v[j][u][e]);
 #pragma unroll
-        for (int h = 0; h < G; ++h) {
-          const float p = __shfl(sc[j][h & 3], tok + 16 * (h >> 2), 64);
+        for (int h2 = 0; h2 < (G + 1) / 2; ++h2) {
+          const uint32_t pp = static_cast<uint32_t>(__shfl(static_cast<int>(pk[j][h2 & 1]), tok + 16 * (h2 >> 1), 64));
+          const f16x2 p2 = __builtin_bit_cast(f16x2, pp);
+          const float p0 = static_cast<float>(p2.x), p1 = static_cast<float>(p2.y);
 #pragma unroll
-          for (int e = 0; e < 8; ++e) acc[h][e] = fmaf(p, vf[e], acc[h][e]);
+          for (int e = 0; e < 8; ++e) acc[2 * h2][e] = fmaf(p0, vf[e], acc[2 * h2][e]);
+          if (2 * h2 + 1 < G) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[2 * h2 + 1][e] = fmaf(p1, vf[e], acc[2 * h2 + 1][e]);
+          }
         }
       }
     }

@@ -315,14 +315,15 @@ def test_fused_qkv_decode_attention_matches_epilogue_then_attention(device, batc
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
-@pytest.mark.parametrize("m", [1, 8, 32])
-def test_qgemm_swiglu_matches_gemm_then_epilogue(device, fmt, m):
+@pytest.mark.parametrize("m,k", [(1, 512), (8, 512), (32, 512), (1, 4096), (3, 4096), (8, 4096)])
+def test_qgemm_swiglu_matches_gemm_then_epilogue(device, fmt, m, k):
     """cir_qgemm_swiglu over interleaved gate/up tiles == cir_qgemm (splits 1) + cir_epilogue_swiglu, bitwise,
-    and within the fp16 bound of the fp64 oracle."""
+    and within the fp16 bound of the fp64 oracle. At m <= 8 the reference side runs the GEMV (k = 4096 stages
+    all of an 8-row activation in 64 KiB of LDS), so the two kernels' partials are compared bit for bit too."""
     from cacheir_amd import kernels
 
-    rng = np.random.default_rng(11 + m)
-    inter, k = 160, 512
+    rng = np.random.default_rng(11 + m + k)
+    inter = 160
     enc = quant.random_q4_0 if fmt == "q4_0" else quant.random_q8_0
     dec = quant.decode_q4_0 if fmt == "q4_0" else quant.decode_q8_0
     code = kernels.FMT_NAMES[fmt]
@@ -463,15 +464,16 @@ def test_row_kernels(device):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("fmt", ["q4_0", "q8_0", "i4_row", "i8_row"])
-@pytest.mark.parametrize("m", [1, 5, 16, 17, 32])
-def test_qgemm_argmax_matches_gemm_then_argmax(device, fmt, m):
+@pytest.mark.parametrize("m,k", [(1, 256), (5, 256), (8, 256), (16, 256), (17, 256), (32, 256), (2, 4096), (8, 4096)])
+def test_qgemm_argmax_matches_gemm_then_argmax(device, fmt, m, k):
     """cir_qgemm_argmax (LM head + greedy argmax, no logits stored) == the oracle's greedy pick over the logits
     of cir_qgemm (splits 1): bitwise the same ids, with a planted tie between a near and a far column (first
-    index wins), a row of NaN logits (numpy picks the first NaN, index 0) and a ragged vocabulary."""
+    index wins), a row of NaN logits (numpy picks the first NaN, index 0) and a ragged vocabulary. Block formats
+    at m <= 8 run the GEMV's argmax epilogue, the rest the GEMM's."""
     from cacheir_amd import kernels
 
-    rng = np.random.default_rng(17 * m + len(fmt))
-    n, k = 1000, 256  # n not a multiple of the 32- or 64-column wavefront groups
+    rng = np.random.default_rng(17 * m + len(fmt) + k)
+    n = 1000  # not a multiple of the 32- or 64-column wavefront groups
     if fmt in ("q4_0", "q8_0"):
         enc = quant.random_q4_0 if fmt == "q4_0" else quant.random_q8_0
         blocks = enc(rng, n, k)[0].reshape(n, -1)

@@ -22,7 +22,9 @@ kernel, launches captured in a HIP graph so no host gap is timed, rotated over t
 layers' KV so the 256 MB MALL cannot hold it), the same for the largest projection (the
 fused gate|up Q4_0 GEMM + SwiGLU at m = batch, rotated
 over the 32 layers' weights), the same for the dequant GEMV at m = 1 and 8 (BASELINE
-config 3's 14336 -> 4096 projection, rotated over the layers' down weights), and a CPU baseline (the C/OpenMP oracle restatement timed on this
+config 3's 14336 -> 4096 projection, rotated over the layers' down weights), the same decode
+step at batch 1 (decode_batch1: the projections and greedy head then run the GEMV), and a CPU
+baseline (the C/OpenMP oracle restatement timed on this
 host over one layer and the lm_head, scaled to a full step).
 
 roofline.traffic is the HBM bytes per attention launch measured by rocprofv3
@@ -121,6 +123,36 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+def time_greedy_steps(plan, steps: int, warmup: int) -> float:
+    """ms per greedy decode step of `plan`: the step (and the copy of its ids into the next step's input) captured
+    in one HIP graph, `warmup` untimed replays, then `steps` replays between two events."""
+    import torch
+
+    def body():
+        plan.launch_greedy()
+        plan.ids.copy_(plan.next_ids)
+
+    # capture (warm-up on a side stream first, as torch requires)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        body()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        body()
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1:
@@ -180,31 +212,7 @@ def main() -> int:
     torch.cuda.synchronize()
     assert torch.equal(plan.next_ids, want), "fused greedy head disagrees with argmax(logits)"
 
-    def body():
-        plan.launch_greedy()
-        plan.ids.copy_(plan.next_ids)
-
-    # capture (warm-up on a side stream first, as torch requires)
-    side = torch.cuda.Stream()
-    side.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(side):
-        body()
-    torch.cuda.current_stream().wait_stream(side)
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        body()
-    for _ in range(args.warmup):
-        graph.replay()
-    torch.cuda.synchronize()
-    log("warm-up done")
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    start.record()
-    for _ in range(args.steps):
-        graph.replay()
-    end.record()
-    torch.cuda.synchronize()
-    ms_step = start.elapsed_time(end) / args.steps
+    ms_step = time_greedy_steps(plan, args.steps, args.warmup)
     toks = B * 1000.0 / ms_step
     assert bool(((plan.next_ids >= 0) & (plan.next_ids < cfg.vocab_size)).all().item()), "ids out of range"
     log(f"step {ms_step:.3f} ms -> {toks:.1f} tok/s")
@@ -252,6 +260,13 @@ def main() -> int:
                      "bytes_per_launch": by, "achieved": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)})
         log(f"GEMV m={m} {dn[0].n}x{dn[0].k} {us:.2f} us/launch, {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%} of peak)")
 
+    # ---- the same decode step at batch 1 (sequence 0's context): QKV, O, down and the greedy head run the GEMV ----
+    plan1 = base.plan("decode", 1, 1, max_pages)
+    plan1.set_inputs(ids[:1], rows[:1], np.full(1, ctx - 1, np.int32))
+    ms_b1 = time_greedy_steps(plan1, args.steps, args.warmup)
+    kv_b1 = 2 * Hkv * D * 2 * ctx * cfg.num_layers
+    log(f"batch-1 step {ms_b1:.3f} ms -> {1000.0 / ms_b1:.1f} tok/s")
+
     traffic = measured_traffic(TRAFFIC_FILE)
 
     # ---- CPU baseline: C/OpenMP restatement, one layer + lm_head, scaled to the step ----
@@ -295,6 +310,9 @@ def main() -> int:
                           "peak": HBM_PEAK_GBS, "unit": "GB/s", "shapes": gemv},
         "step_bytes": {"weights": weight_bytes, "kv": kv_bytes * cfg.num_layers,
                        "hbm_floor_ms": round((weight_bytes + kv_bytes * cfg.num_layers) / HBM_PEAK_GBS / 1e6, 4)},
+        "decode_batch1": {"ms_per_step": round(ms_b1, 4), "tokens_per_s": round(1000.0 / ms_b1, 2),
+                          "hbm_floor_ms": round((weight_bytes + kv_b1) / HBM_PEAK_GBS / 1e6, 4),
+                          "note": "same model and context, one sequence; projections on the dequant GEMV"},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

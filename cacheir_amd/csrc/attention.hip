@@ -535,12 +535,15 @@ int max_splits(int max_context) { return max(1, (max_context + kMinSplitTokens -
 
 int generic_chunks(int max_context) { return max(1, (max_context + kChunk - 1) / kChunk); }
 
-// Splits for the fp16 path: 1 when rows*kv_heads workgroups of 8 wavefronts already
-// cover the 256 CUs; otherwise enough to reach about 320 workgroups.
+// Splits for the fp16 path: about one workgroup per CU (256 / (rows * kv_heads)),
+// at most 8.  Measured at 2048 tokens of context, 32/8 heads (attention + merge):
+// batch 1 best at 8 splits (13.1 us; 16 splits 14.8, 64 splits 34), batch 4 at 4-8,
+// batch 8 at 4 (19.7 us; 8 splits 25.3), batch 16 at 2 (29.5 us; 1 split 32.8,
+// 4 splits 33.9), batch 32 at 1.  More splits add per-workgroup fixed cost (page
+// table, q, first load latency, the 8-wavefront merge) and a longer merge.
 int choose_splits(int rows, int Hkv, int max_context) {
   const long groups = (long)rows * Hkv;
-  if (groups >= 160) return 1;
-  const int want = (int)((320 + groups - 1) / groups);
+  const int want = (int)min(8L, max(1L, 256 / groups));
   return max(1, min(want, max_splits(max_context)));
 }
 

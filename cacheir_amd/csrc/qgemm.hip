@@ -607,6 +607,215 @@ __device__ __forceinline__ uint2 buf8(rsrc_t r, uint32_t voff, uint32_t soff) {
   const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0);
   return uint2{v.x, v.y};
 }
+// 16 bytes per lane from the buffer straight into LDS: lane l's bytes land at lds + 16 l.
+// (A device function, not a lambda: kernel lambdas are also compiled for the host,
+// where the builtin does not exist, and the host pass then drops the kernel's stub.)
+__device__ __forceinline__ void buf16_to_lds(rsrc_t r, uint8_t* lds, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, soff, 0, 0);
+}
+
+// ------------------------------------------------------------- large m ------
+// m > 32 (qgemm_xl_kernel): a workgroup of 4 wavefronts covers 8 weight tiles (128
+// output columns, 2 per wavefront) and 16*MT activation rows, so each weight tile is
+// read once per 16*MT rows (the m <= 32 kernel reads it once per 32).  A quad of
+// activations (16*MT rows x 128 columns fp16, 4 KiB per 16 rows) goes straight to
+// LDS by buffer DMA (no registers), double-buffered, one barrier per quad.  Chunk g
+// (16 B) of row r sits in slot g ^ (r & 15) of the row's 256 B, so the 16 rows of a
+// fragment read hit 16 different bank groups.  Weights stream through a ring of
+// DW + 1 slots as in the GEMV.  Per tile and quad the blocks are scaled and summed in
+// the m <= 32 kernel's order, so for the same split both give the same bits.
+// EPI 0: fp32 split-k partials part[split][m][n]; EPI 1: SwiGLU over interleaved
+// gate/up tiles (one split), out[m][N/2] in type TO.
+template <int FMT, int MT, int DW, int EPI = 0, typename TO = float>
+__global__ __launch_bounds__(256) void qgemm_xl_kernel(const f16* __restrict__ x, int ldx,
+                                                     const uint8_t* __restrict__ wq, const uint16_t* __restrict__ wd,
+                                                     float* __restrict__ part, int M, int N, int K, int nq,
+                                                     TO* __restrict__ act = nullptr) {
+  static_assert(EPI == 0 || EPI == 1, "large-m GEMM epilogues: partials or SwiGLU");
+  constexpr int NT = 2;
+  constexpr int LB = Stage<FMT, NT, 1>::LB;
+  constexpr int kSlot = 16 * MT * 256;  // bytes of one quad of activations
+  __shared__ __align__(16) uint8_t smem[2 * kSlot];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63, li = lane & 15, lg = lane >> 4;
+  const int KQ = K / 128, NTILES = (N + 15) / 16;
+  const int nt0 = (blockIdx.x * 4 + wave) * NT;
+  const int split = blockIdx.y;
+  const int m0 = blockIdx.z * 16 * MT;
+  const int q0 = split * nq;
+
+  // Activation DMA: instruction u (0..MT-1) of wavefront w fills LDS bytes
+  // [(w*MT + u) KiB, +1 KiB) of a slot, 16 B per lane: row r = 4 (w*MT + u) + lane/16,
+  // slot s = lane % 16 holds chunk s ^ (r & 15).  Rows past M re-read row M-1.
+  const rsrc_t rx = make_rsrc(x, (uint32_t)((size_t)M * ldx * 2));
+  uint32_t xoff[MT];
+#pragma unroll
+  for (int u = 0; u < MT; ++u) {
+    const int r = 4 * (wave * MT + u) + (lane >> 4);
+    const int g = (lane & 15) ^ (r & 15);
+    xoff[u] = (uint32_t)min(m0 + r, M - 1) * (uint32_t)ldx * 2u + 16u * g;
+  }
+  auto dma_x = [&](int slot, int Q) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < MT; ++u)
+      buf16_to_lds(rx, smem + slot * kSlot + (wave * MT + u) * 1024, xoff[u], 256u * (uint32_t)(q0 + Q));
+  };
+
+  const uint32_t ntiles_total = (uint32_t)NTILES * KQ;
+  const rsrc_t rw = make_rsrc(wq, ntiles_total * 1024u * LB);
+  const rsrc_t rd = make_rsrc(wd, is_row_fmt(FMT) ? 0u : ntiles_total * 128u);
+  uint32_t tb[NT];
+#pragma unroll
+  for (int b = 0; b < NT; ++b) tb[b] = (uint32_t)min(nt0 + b, NTILES - 1) * KQ + q0;
+  const uint32_t vw = (uint32_t)lane * 16u * LB, vd = (uint32_t)li * 8u;
+  struct WS {
+    uint4 w[NT][LB];
+    uint2 d[NT];
+  };
+  constexpr int R = DW + 1;
+  WS ws[R];
+  auto issue = [&](int slot, int idx) __attribute__((always_inline)) {  // quad idx, clamped to the last
+    const uint32_t Q = (uint32_t)min(idx, nq - 1);
+#pragma unroll
+    for (int b = 0; b < NT; ++b) {
+#pragma unroll
+      for (int c = 0; c < LB; ++c) ws[slot].w[b][c] = buf16(rw, vw + 16u * c, (tb[b] + Q) * 1024u * LB);
+      if constexpr (!is_row_fmt(FMT)) ws[slot].d[b] = buf8(rd, vd, (tb[b] + Q) * 128u);
+    }
+  };
+  auto each = [&]<int C>(auto&& f) __attribute__((always_inline)) {
+    [&]<int... S>(std::integer_sequence<int, S...>) { (f.template operator()<S>(), ...); }(
+        std::make_integer_sequence<int, C>{});
+  };
+
+  f32x4 acc[MT][NT];
+  f32x4 sx[MT];  // row formats: activation sums of this split
+#pragma unroll
+  for (int a = 0; a < MT; ++a) {
+    sx[a] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int b = 0; b < NT; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  int xo[4];  // swizzled byte offset of chunk 4j + lg in row 16a + li (li & 15 = li)
+#pragma unroll
+  for (int j = 0; j < 4; ++j) xo[j] = li * 256 + (((4 * j + lg) ^ li) << 4);
+
+  auto compute = [&](const WS& st, int xslot) __attribute__((always_inline)) {
+    f16x8 wb[NT][4];
+    float dj[NT][4];
+#pragma unroll
+    for (int b = 0; b < NT; ++b)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if constexpr (layout_fmt(FMT) == CIR_Q4_0) {
+          const uint4 v = st.w[b][0];
+          wb[b][j] = dq_q4((j == 0) ? v.x : (j == 1) ? v.y : (j == 2) ? v.z : v.w);
+        } else {
+          const uint4 v = st.w[b][j >> 1];
+          wb[b][j] = dq_q8((j & 1) ? v.z : v.x, (j & 1) ? v.w : v.y);
+        }
+        if constexpr (!is_row_fmt(FMT)) {
+          const uint32_t dw = (j < 2) ? st.d[b].x : st.d[b].y;
+          dj[b][j] = static_cast<float>(__builtin_bit_cast(f16, (uint16_t)((j & 1) ? (dw >> 16) : (dw & 0xFFFFu))));
+        }
+      }
+    const uint8_t* xq = smem + xslot * kSlot;
+#pragma unroll
+    for (int a = 0; a < MT; ++a) {
+      f16x8 xf[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) xf[j] = *reinterpret_cast<const f16x8*>(xq + a * 4096 + xo[j]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if constexpr (is_row_fmt(FMT)) {
+#pragma unroll
+          for (int b = 0; b < NT; ++b) acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xf[j], wb[b][j], acc[a][b], 0, 0, 0);
+          const f16x8 ones = {1, 1, 1, 1, 1, 1, 1, 1};
+          sx[a] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xf[j], ones, sx[a], 0, 0, 0);
+        } else {
+          f32x4 c[NT];
+#pragma unroll
+          for (int b = 0; b < NT; ++b)
+            c[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xf[j], wb[b][j], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+          for (int b = 0; b < NT; ++b)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[a][b][r] = fmaf(dj[b][j], c[b][r], acc[a][b][r]);
+        }
+      }
+    }
+  };
+
+  auto barrier = [] { __syncthreads(); };
+  // Prologue: activations of quad 0 (slot 0) and weight stages 0 .. DW-1 in flight.
+  dma_x(0, 0);
+  each.template operator()<DW>([&]<int S>() { issue(S, S); });
+  barrier();  // (the compiler waits for this wavefront's DMA before the barrier)
+  // Stage i: compute quad i, then DMA quad i+1 into the other slot and refill the ring,
+  // then the barrier that publishes quad i+1 (and frees slot i & 1).  The DMA goes out
+  // after the compute's LDS reads: issued before them, the compiler (which cannot tell
+  // the two slots apart) would wait for it, and for every load issued after it.  The
+  // wait before the barrier covers the DMA but not the weights issued after it.
+  int i = 0;
+#pragma nounroll
+  for (; i + R <= nq; i += R) {
+    each.template operator()<R>([&]<int S>() {
+      compute(ws[S], (i + S) & 1);
+      dma_x((i + S + 1) & 1, min(i + S + 1, nq - 1));
+      issue((S + DW) % R, i + S + DW);
+      barrier();
+    });
+  }
+  each.template operator()<DW>([&]<int S>() {  // at most DW quads are left, in ring slots 0 .. DW-1
+    if (i + S < nq) {
+      compute(ws[S], (i + S) & 1);
+      dma_x((i + S + 1) & 1, min(i + S + 1, nq - 1));
+      barrier();
+    }
+  });
+
+  if constexpr (is_row_fmt(FMT)) {
+    const float* rscale = reinterpret_cast<const float*>(wd);
+    const float* roff = rscale + (size_t)NTILES * 16;
+#pragma unroll
+    for (int b = 0; b < NT; ++b) {
+      const int n = min(nt0 + b, NTILES - 1) * 16 + li;
+      const float sc = rscale[n], of = roff[n];
+#pragma unroll
+      for (int a = 0; a < MT; ++a)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[a][b][r] = sc * fmaf(of, sx[a][r], acc[a][b][r]);
+    }
+  }
+  if constexpr (EPI == 1) {
+    const int inter = N / 2;
+    const int col = (nt0 >> 1) * 16 + li;
+    if (nt0 + 1 < NTILES && col < inter) {
+#pragma unroll
+      for (int a = 0; a < MT; ++a)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int m = m0 + 16 * a + 4 * lg + r;
+          const float g = acc[a][0][r], u = acc[a][1][r];
+          if (m < M) act[(size_t)m * inter + col] = static_cast<TO>(as_f32_value((g / (1.0f + expf(-g))) * u));
+        }
+    }
+  } else {
+#pragma unroll
+    for (int a = 0; a < MT; ++a)
+#pragma unroll
+      for (int b = 0; b < NT; ++b) {
+        const int n = (nt0 + b) * 16 + li;
+        if (nt0 + b < NTILES && n < N) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int m = m0 + 16 * a + 4 * lg + r;
+            if (m < M) part[((size_t)split * M + m) * N + n] = acc[a][b][r];
+          }
+        }
+      }
+  }
+}
 
 // m <= 8 (qgemv_kernel): a workgroup of W wavefronts owns W*NT row tiles, and each
 // wavefront streams its own NT tiles over the workgroup's k-range (grid.y splits k)
@@ -1046,6 +1255,40 @@ void launch_qgemm_xs(const f16* x, int ldx, const uint8_t* wq, const uint16_t* w
   }
 }
 
+// Large m: activation rows per workgroup (16 * MT).
+constexpr int xl_mt(int m) { return m <= 64 ? 4 : 8; }
+
+// m > 32 takes the large-m kernel when n spans at least 36 groups of 128 columns.
+// Measured at the Qwen2-7B shapes (Q8_0, m = 64 / 128) against the m <= 32 kernel
+// run over 32-row blocks: QKV (n 4608) 11.0 / 16.9 us against 15.4 / 24.5, gate|up
+// (n 37888) 51.6 / 81.8 against 72.6 / 114.9; but O and down (n 3584, 28 groups)
+// lose (O 14.3 against 13.4 us at m = 128, down 79 against 56): too few column
+// groups to fill the CUs without many more k-splits.
+bool use_xl(int m, int n) { return m > 32 && (n + 127) / 128 >= 36; }
+
+// Its k-split: the smallest divisor of k/128 (not only powers of two) giving >= 192
+// workgroups, keeping at least 4 quads per split.
+int xl_splits(int m, int n, int k) {
+  const int kq = k / 128;
+  const long groups = (long)((n + 127) / 128) * ((m + 16 * xl_mt(m) - 1) / (16 * xl_mt(m)));
+  int best = 1;
+  for (int s = 1; s <= kq / 4; ++s) {
+    if (kq % s) continue;
+    best = s;
+    if (groups * s >= 192) break;
+  }
+  return best;
+}
+
+template <int FMT, int MT, int EPI, typename TO = float>
+void launch_qgemm_xl(const f16* x, int ldx, const uint8_t* wq, const uint16_t* wd, float* part, int M, int N, int K,
+                     int splits, hipStream_t s, TO* act = nullptr) {
+  constexpr int DW = layout_fmt(FMT) == CIR_Q4_0 ? 4 : 3;
+  const int NTILES = (N + 15) / 16;
+  dim3 grid((NTILES + 7) / 8, splits, (M + 16 * MT - 1) / (16 * MT));
+  qgemm_xl_kernel<FMT, MT, DW, EPI, TO><<<grid, 256, 0, s>>>(x, ldx, wq, wd, part, M, N, K, (K / 128) / splits, act);
+}
+
 // Workgroup rows: 4 wavefronts x NT tiles x 16.  m <= 16 takes NT = 1 (64 rows per
 // workgroup, MT = 1); larger m takes NT = 2, MT = 2 (128 rows x 32 activation rows):
 // each activation quad then feeds 8 weight tiles.  Measured on MI355X at the
@@ -1058,6 +1301,7 @@ int default_splits(int m, int n, int k) {
   if (m <= 8) {
     if (const int s = gemv_splits(m, n, k)) return s;
   }
+  if (use_xl(m, n)) return xl_splits(m, n, k);
   const int kq = k / 128;
   const long groups = (long)((n + xs_rows_per_group(m) - 1) / xs_rows_per_group(m)) * ((m + 31) / 32);
   int s = 1;
@@ -1070,7 +1314,9 @@ void dispatch_qgemm(const f16* x, int ldx, const uint8_t* wq, const uint16_t* wd
                     int splits, hipStream_t s) {
   if (gemv_fits(M, K, splits)) launch_qgemv<FMT, 0>(x, ldx, wq, wd, part, M, N, K, splits, s);
   else if (M <= 16) launch_qgemm_xs<FMT, 1, 1, 4>(x, ldx, wq, wd, part, M, N, K, splits, s);
-  else launch_qgemm_xs<FMT, 2, 2, CIR_XS_DW>(x, ldx, wq, wd, part, M, N, K, splits, s);
+  else if (!use_xl(M, N)) launch_qgemm_xs<FMT, 2, 2, CIR_XS_DW>(x, ldx, wq, wd, part, M, N, K, splits, s);
+  else if (M <= 64) launch_qgemm_xl<FMT, 4, 0>(x, ldx, wq, wd, part, M, N, K, splits, s);
+  else launch_qgemm_xl<FMT, 8, 0>(x, ldx, wq, wd, part, M, N, K, splits, s);
 }
 
 }  // namespace
@@ -1191,6 +1437,15 @@ extern "C" int cir_qgemm_swiglu(const void* x, int ldx, const void* w_tiled, int
   const f16* xh = static_cast<const f16*>(x);
   hipStream_t s = as_stream(stream);
   auto go = [&]<int FMT>() {
+    if (use_xl(m, n)) {
+      auto xl = [&]<int MT>() {
+        if (odt == CIR_F16) launch_qgemm_xl<FMT, MT, 1, f16>(xh, ldx, q, d, nullptr, m, n, k, 1, s, static_cast<f16*>(out));
+        else launch_qgemm_xl<FMT, MT, 1, float>(xh, ldx, q, d, nullptr, m, n, k, 1, s, static_cast<float*>(out));
+      };
+      if (xl_mt(m) == 4) xl.template operator()<4>();
+      else xl.template operator()<8>();
+      return;
+    }
     if (odt == CIR_F16) {
       if (m <= 16) launch_qgemm_swiglu<FMT, 1>(xh, ldx, q, d, static_cast<f16*>(out), m, n, k, s);
       else launch_qgemm_swiglu<FMT, 2>(xh, ldx, q, d, static_cast<f16*>(out), m, n, k, s);

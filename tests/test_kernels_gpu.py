@@ -136,7 +136,9 @@ def test_dequant_bit_exact(device, fmt):
 
 @pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
 @pytest.mark.parametrize("m,n,k,splits", [(1, 64, 128, 1), (5, 100, 256, 2), (16, 48, 512, 4), (32, 80, 384, 3),
-                                          (33, 16, 128, 1), (70, 40, 256, 1)])
+                                          (33, 16, 128, 1), (70, 40, 256, 1), (64, 48, 256, 2), (128, 100, 512, 4),
+                                          (100, 200, 1280, 5), (200, 24, 384, 3), (64, 4608, 512, 1),
+                                          (128, 4610, 896, 7), (150, 4608, 384, 3)])
 def test_qgemm_small(device, fmt, m, n, k, splits):
     from cacheir_amd import kernels
 
@@ -315,7 +317,8 @@ def test_fused_qkv_decode_attention_matches_epilogue_then_attention(device, batc
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
-@pytest.mark.parametrize("m,k", [(1, 512), (8, 512), (32, 512), (1, 4096), (3, 4096), (8, 4096)])
+@pytest.mark.parametrize("m,k", [(1, 512), (8, 512), (32, 512), (48, 512), (128, 640), (1, 4096), (3, 4096),
+                                 (8, 4096)])
 def test_qgemm_swiglu_matches_gemm_then_epilogue(device, fmt, m, k):
     """cir_qgemm_swiglu over interleaved gate/up tiles == cir_qgemm (splits 1) + cir_epilogue_swiglu, bitwise,
     and within the fp16 bound of the fp64 oracle. At m <= 8 the reference side runs the GEMV (k = 4096 stages
@@ -323,7 +326,7 @@ def test_qgemm_swiglu_matches_gemm_then_epilogue(device, fmt, m, k):
     from cacheir_amd import kernels
 
     rng = np.random.default_rng(11 + m + k)
-    inter = 160
+    inter = 160 if m <= 32 else 2304  # m > 32: wide enough (n 4608) for the large-m kernel
     enc = quant.random_q4_0 if fmt == "q4_0" else quant.random_q8_0
     dec = quant.decode_q4_0 if fmt == "q4_0" else quant.decode_q8_0
     code = kernels.FMT_NAMES[fmt]
@@ -431,13 +434,23 @@ def test_row_packed_dequant_bit_exact_and_gemm(device, bits):
     deq = quant.asymmetric_dequant(pk)
     got = kernels.dequant_tiled(qw).cpu().numpy()
     assert np.array_equal(got.view(np.uint32), deq.astype(np.float32).view(np.uint32))
-    for m in (1, 8, 32):
+    for m in (1, 8, 32, 64, 128):
         x = rng.standard_normal((m, k)).astype(np.float16)
         for splits in (1, 3):
             y = kernels.qgemm_partial(to_dev(x, device), qw, splits=splits).sum(0).double().cpu().numpy()
             ref = x.astype(np.float64) @ deq.astype(np.float64).T
             err = np.abs(y - ref) - (2e-3 + 1e-2 * np.abs(ref))
             assert np.all(err <= 0), (m, splits, err.max())
+    # n 4608 at m 128: the large-m kernel (row scales after the k loop, activation sums by MFMA)
+    n2, k2 = 4608, 256
+    w2 = rng.standard_normal((n2, k2)).astype(np.float32) * 0.05
+    pk2 = quant.asymmetric_pack(w2, bits)
+    qw2 = kernels.QWeight.from_rows(to_dev(pk2["packed_values"], device), to_dev(pk2["scales"], device),
+                                    to_dev(pk2["zero_points"], device), bits, n2, k2)
+    x2 = rng.standard_normal((128, k2)).astype(np.float16)
+    y2 = kernels.qgemm_partial(to_dev(x2, device), qw2).sum(0).double().cpu().numpy()
+    ref2 = x2.astype(np.float64) @ quant.asymmetric_dequant(pk2).astype(np.float64).T
+    assert np.all(np.abs(y2 - ref2) - (2e-3 + 1e-2 * np.abs(ref2)) <= 0)
 
 
 def test_row_kernels(device):

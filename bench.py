@@ -22,7 +22,9 @@ kernel, launches captured in a HIP graph so no host gap is timed, rotated over t
 layers' KV so the 256 MB MALL cannot hold it), the same for the largest projection (the
 fused gate|up Q4_0 GEMM + SwiGLU at m = batch, rotated
 over the 32 layers' weights), the same for the dequant GEMV at m = 1 and 8 (BASELINE
-config 3's 14336 -> 4096 projection, rotated over the layers' down weights), the same decode
+config 3's 14336 -> 4096 projection, rotated over the layers' down weights), the batched GEMM
+on MFMA (BASELINE config 5's Q8_0 gate|up + SwiGLU at batch 128: TFLOP/s against the dense fp16
+MFMA peak), the same decode
 step at batch 1 (decode_batch1: the projections and greedy head then run the GEMV), and a CPU
 baseline (the C/OpenMP oracle restatement timed on this
 host over one layer and the lm_head, scaled to a full step).
@@ -44,6 +46,7 @@ import time
 import numpy as np
 
 HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0  # dense fp16 MFMA, MI355X
 TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                             "attn_f16_d128_decode_b32_ctx2048_traffic.txt")
 
@@ -260,6 +263,28 @@ def main() -> int:
                      "bytes_per_launch": by, "achieved": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)})
         log(f"GEMV m={m} {dn[0].n}x{dn[0].k} {us:.2f} us/launch, {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%} of peak)")
 
+    # ---- the batched GEMM on MFMA: BASELINE config 5's gate|up (Qwen2-7B, Q8_0) + SwiGLU at batch 128 ----
+    n5, k5, m5 = 2 * 18944, 3584, 128
+
+    def random_q8_0(seed: int):
+        g5 = torch.Generator(device=dev)
+        g5.manual_seed(seed)
+        nb = n5 * (k5 // 32)
+        blocks = torch.randint(0, 256, (nb, 34), dtype=torch.uint8, device=dev, generator=g5)
+        d = (torch.rand(nb, device=dev, generator=g5) * 0.02 + 0.001).half()
+        blocks[:, :2] = d.view(torch.uint8).view(nb, 2)
+        return kernels.QWeight.from_blocks(blocks.reshape(-1), kernels.FMT_NAMES["q8_0"], n5, k5)
+
+    w5 = [random_q8_0(100 + i) for i in range(4)]  # 4 x 144 MB: rotated past the 256 MB MALL
+    x5 = torch.randn((m5, k5), device=dev, dtype=torch.float16)
+    o5 = torch.empty((m5, n5 // 2), device=dev, dtype=torch.float16)
+    us5 = graph_us_per_launch(lambda it: kernels.qgemm_swiglu(x5, w5[it % len(w5)], out=o5), args.gemm_iters)
+    tflops5 = 2.0 * m5 * n5 * k5 / (us5 * 1e-6) / 1e12
+    gbs5 = (w5[0].nbytes + 2 * m5 * k5 + 2 * m5 * (n5 // 2)) / (us5 * 1e-6) / 1e9
+    log(f"batched GEMM (config 5 gate|up Q8_0, m={m5}) {us5:.2f} us/launch, {tflops5:.0f} TFLOP/s "
+        f"({tflops5 / MFMA_F16_PEAK_TFLOPS:.1%} of fp16 MFMA), {gbs5:.0f} GB/s")
+    del w5
+
     # ---- the same decode step at batch 1 (sequence 0's context): QKV, O, down and the greedy head run the GEMV ----
     plan1 = base.plan("decode", 1, 1, max_pages)
     plan1.set_inputs(ids[:1], rows[:1], np.full(1, ctx - 1, np.int32))
@@ -308,6 +333,12 @@ def main() -> int:
                           "us_per_launch": round(gemm_us, 3)},
         "roofline_gemv": {"bound": "hbm", "kernel": "Q4_0 dequant GEMV (qgemv_kernel), BASELINE config 3 down shape",
                           "peak": HBM_PEAK_GBS, "unit": "GB/s", "shapes": gemv},
+        "roofline_batched_gemm": {"bound": "mfma",
+                                  "kernel": "Q8_0 gate|up GEMM + SwiGLU m=128 (qgemm_xl_kernel, EPI=1), "
+                                            "BASELINE config 5 shape (n 37888, k 3584)",
+                                  "achieved": round(tflops5, 1), "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                                  "frac": round(tflops5 / MFMA_F16_PEAK_TFLOPS, 4), "us_per_launch": round(us5, 3),
+                                  "hbm_gbs": round(gbs5, 1)},
         "step_bytes": {"weights": weight_bytes, "kv": kv_bytes * cfg.num_layers,
                        "hbm_floor_ms": round((weight_bytes + kv_bytes * cfg.num_layers) / HBM_PEAK_GBS / 1e6, 4)},
         "decode_batch1": {"ms_per_step": round(ms_b1, 4), "tokens_per_s": round(1000.0 / ms_b1, 2),

@@ -626,8 +626,8 @@ __device__ __forceinline__ void buf16_to_lds(rsrc_t r, uint8_t* lds, uint32_t vo
 // the m <= 32 kernel's order, so for the same split both give the same bits.
 // EPI 0: fp32 split-k partials part[split][m][n]; EPI 1: SwiGLU over interleaved
 // gate/up tiles (one split), out[m][N/2] in type TO.
-template <int FMT, int MT, int DW, int EPI = 0, typename TO = float>
-__global__ __launch_bounds__(256) void qgemm_xl_kernel(const f16* __restrict__ x, int ldx,
+template <int FMT, int MT, int DW, int EPI = 0, typename TO = float, int W = 4>
+__global__ __launch_bounds__(64 * W) void qgemm_xl_kernel(const f16* __restrict__ x, int ldx,
                                                      const uint8_t* __restrict__ wq, const uint16_t* __restrict__ wd,
                                                      float* __restrict__ part, int M, int N, int K, int nq,
                                                      TO* __restrict__ act = nullptr) {
@@ -639,26 +639,28 @@ __global__ __launch_bounds__(256) void qgemm_xl_kernel(const f16* __restrict__ x
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63, li = lane & 15, lg = lane >> 4;
   const int KQ = K / 128, NTILES = (N + 15) / 16;
-  const int nt0 = (blockIdx.x * 4 + wave) * NT;
+  const int nt0 = (blockIdx.x * W + wave) * NT;
   const int split = blockIdx.y;
   const int m0 = blockIdx.z * 16 * MT;
   const int q0 = split * nq;
 
-  // Activation DMA: instruction u (0..MT-1) of wavefront w fills LDS bytes
-  // [(w*MT + u) KiB, +1 KiB) of a slot, 16 B per lane: row r = 4 (w*MT + u) + lane/16,
+  // Activation DMA: instruction u (0..XU-1) of wavefront w fills LDS bytes
+  // [(w*XU + u) KiB, +1 KiB) of a slot, 16 B per lane: row r = 4 (w*XU + u) + lane/16,
   // slot s = lane % 16 holds chunk s ^ (r & 15).  Rows past M re-read row M-1.
+  constexpr int XU = 4 * MT / W;  // KiB of a quad each wavefront brings in
+  static_assert(XU * W == 4 * MT, "the wavefronts split a quad of activations evenly");
   const rsrc_t rx = make_rsrc(x, (uint32_t)((size_t)M * ldx * 2));
-  uint32_t xoff[MT];
+  uint32_t xoff[XU];
 #pragma unroll
-  for (int u = 0; u < MT; ++u) {
-    const int r = 4 * (wave * MT + u) + (lane >> 4);
+  for (int u = 0; u < XU; ++u) {
+    const int r = 4 * (wave * XU + u) + (lane >> 4);
     const int g = (lane & 15) ^ (r & 15);
     xoff[u] = (uint32_t)min(m0 + r, M - 1) * (uint32_t)ldx * 2u + 16u * g;
   }
   auto dma_x = [&](int slot, int Q) __attribute__((always_inline)) {
 #pragma unroll
-    for (int u = 0; u < MT; ++u)
-      buf16_to_lds(rx, smem + slot * kSlot + (wave * MT + u) * 1024, xoff[u], 256u * (uint32_t)(q0 + Q));
+    for (int u = 0; u < XU; ++u)
+      buf16_to_lds(rx, smem + slot * kSlot + (wave * XU + u) * 1024, xoff[u], 256u * (uint32_t)(q0 + Q));
   };
 
   const uint32_t ntiles_total = (uint32_t)NTILES * KQ;
@@ -1280,13 +1282,18 @@ int xl_splits(int m, int n, int k) {
   return best;
 }
 
+#ifndef CIR_XL_W
+#define CIR_XL_W 4
+#endif
 template <int FMT, int MT, int EPI, typename TO = float>
 void launch_qgemm_xl(const f16* x, int ldx, const uint8_t* wq, const uint16_t* wd, float* part, int M, int N, int K,
                      int splits, hipStream_t s, TO* act = nullptr) {
   constexpr int DW = layout_fmt(FMT) == CIR_Q4_0 ? 4 : 3;
+  constexpr int W = CIR_XL_W;
   const int NTILES = (N + 15) / 16;
-  dim3 grid((NTILES + 7) / 8, splits, (M + 16 * MT - 1) / (16 * MT));
-  qgemm_xl_kernel<FMT, MT, DW, EPI, TO><<<grid, 256, 0, s>>>(x, ldx, wq, wd, part, M, N, K, (K / 128) / splits, act);
+  dim3 grid((NTILES + 2 * W - 1) / (2 * W), splits, (M + 16 * MT - 1) / (16 * MT));
+  qgemm_xl_kernel<FMT, MT, DW, EPI, TO, W>
+      <<<grid, 64 * W, 0, s>>>(x, ldx, wq, wd, part, M, N, K, (K / 128) / splits, act);
 }
 
 // Workgroup rows: 4 wavefronts x NT tiles x 16.  m <= 16 takes NT = 1 (64 rows per

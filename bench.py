@@ -19,7 +19,9 @@ every step re-appends at the same slot and attends over exactly 2048 tokens.
 Printed: one JSON line with value = decode tokens/s (32 tokens per step), the
 paged-attention roofline (algorithmic bytes / live HIP-event time of the attention
 kernel, launches captured in a HIP graph so no host gap is timed, rotated over the 32
-layers' KV so the 256 MB MALL cannot hold it), the same for the largest projection (the
+layers' KV so the 256 MB MALL cannot hold it), the same kernel at BASELINE configs 2 and 5
+(ragged contexts over randomly permuted pages; config 5 with a shared 1024-token prefix, its
+bytes counted once), the same for the largest projection (the
 fused gate|up Q4_0 GEMM + SwiGLU at m = batch, rotated
 over the 32 layers' weights), the same for the dequant GEMV at m = 1 and 8 (BASELINE
 config 3's 14336 -> 4096 projection, rotated over the layers' down weights), the batched GEMM
@@ -156,6 +158,74 @@ def time_greedy_steps(plan, steps: int, warmup: int) -> float:
     return start.elapsed_time(end) / steps
 
 
+def ragged_attention_case(config: int, dev, iters: int) -> dict:
+    """Paged decode attention at BASELINE config 2 (batch 64, Llama-3-8B heads, contexts
+    U[512, 4096], pages permuted at random over the pool) or config 5 (batch 128, Qwen2-7B
+    heads, one 1024-token prefix in 64 pages shared by every page table, suffixes U[64, 7168]
+    in pages of their own, permuted).  Context lengths and page tables are numpy draws with
+    seed 0; q and the K/V pools are N(0,1) fp16 drawn on the device.  Two copies of the pools
+    alternate so the 256 MB MALL holds neither.  Returns bytes and live time per launch."""
+    import torch
+
+    from cacheir_amd import kernels
+
+    rng = np.random.default_rng(0)
+    P, D = 16, 128
+    if config == 2:
+        B, H, Hkv = 64, 32, 8
+        ctx = rng.integers(512, 4097, B)
+        npg = -(-ctx // P)
+        slots = int(npg.sum())
+        perm = rng.permutation(slots)
+        max_pages = 4096 // P
+        pt = np.zeros((B, max_pages), np.int32)
+        off = 0
+        for b in range(B):
+            pt[b, : npg[b]] = perm[off: off + npg[b]]
+            off += npg[b]
+        unique_tokens = int(ctx.sum())
+    else:
+        B, H, Hkv, prefix = 128, 28, 4, 1024
+        suffix = rng.integers(64, 7169, B)
+        ctx = prefix + suffix
+        npg = -(-suffix // P)
+        slots = prefix // P + int(npg.sum())
+        perm = prefix // P + rng.permutation(slots - prefix // P)
+        max_pages = (prefix + 7168) // P
+        pt = np.zeros((B, max_pages), np.int32)
+        off = 0
+        for b in range(B):
+            pt[b, : prefix // P] = np.arange(prefix // P)
+            pt[b, prefix // P: prefix // P + npg[b]] = perm[off: off + npg[b]]
+            off += npg[b]
+        unique_tokens = prefix + int(suffix.sum())
+    g = torch.Generator(device=dev)
+    g.manual_seed(config)
+    pools = [(torch.randn((slots, Hkv, P, D), device=dev, generator=g).half(),
+              torch.randn((slots, Hkv, P, D), device=dev, generator=g).half()) for _ in range(2)]
+    q = torch.randn((B, H, D), device=dev, generator=g).half()
+    out = torch.empty_like(q)
+    table = torch.from_numpy(pt).to(dev)
+    lens = torch.from_numpy(ctx.astype(np.int32)).to(dev)
+    ws = kernels.attention_workspace(B, H, D, max_pages * P, dev)
+    us = graph_us_per_launch(lambda it: kernels.paged_decode_attention(
+        q, pools[it % 2][0], pools[it % 2][1], table, lens, out=out, workspace=ws), iters)
+    per_token = 2 * Hkv * D * 2  # K + V, fp16
+    side = 2 * B * H * D * 2 + 4 * int(npg.sum()) + 4 * B  # q, out, page-table entries, lengths
+    unique = per_token * unique_tokens + side
+    logical = per_token * int(ctx.sum()) + side
+    res = {"config": config, "batch": B, "heads": [H, Hkv], "context_sum": int(ctx.sum()),
+           "context_max": int(ctx.max()), "us_per_launch": round(us, 3), "bytes_per_launch": unique,
+           "achieved": round(unique / (us * 1e-6) / 1e9, 1),
+           "frac": round(unique / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+    if config == 5:
+        res["logical_bytes_per_launch"] = logical
+        res["logical_gbs"] = round(logical / (us * 1e-6) / 1e9, 1)
+    del pools
+    torch.cuda.empty_cache()
+    return res
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1:
@@ -285,6 +355,15 @@ def main() -> int:
         f"({tflops5 / MFMA_F16_PEAK_TFLOPS:.1%} of fp16 MFMA), {gbs5:.0f} GB/s")
     del w5
 
+    # ---- the attention kernel at BASELINE configs 2 and 5 (ragged contexts, permuted / shared pages) ----
+    ragged = []
+    for c in (2, 5):
+        r = ragged_attention_case(c, dev, max(8, args.attn_iters // 4))
+        ragged.append(r)
+        extra = f", logical {r['logical_gbs']:.0f} GB/s" if "logical_gbs" in r else ""
+        log(f"attention config {c} (batch {r['batch']}, context sum {r['context_sum']}) {r['us_per_launch']:.2f} "
+            f"us/launch, {r['achieved']:.0f} GB/s unique ({r['frac']:.1%} of peak){extra}")
+
     # ---- the same decode step at batch 1 (sequence 0's context): QKV, O, down and the greedy head run the GEMV ----
     plan1 = base.plan("decode", 1, 1, max_pages)
     plan1.set_inputs(ids[:1], rows[:1], np.full(1, ctx - 1, np.int32))
@@ -327,6 +406,10 @@ def main() -> int:
                      "traffic": traffic["bytes"] if traffic else None,
                      "traffic_detail": traffic,
                      "bytes_per_launch": attn_bytes, "us_per_launch": round(attn_us, 3)},
+        "roofline_attention_ragged": {"bound": "hbm", "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                      "note": "BASELINE configs 2 and 5; achieved on unique K/V bytes (config 5's "
+                                              "shared prefix counted once), logical bytes beside it",
+                                      "cases": ragged},
         "roofline_gemm": {"bound": "hbm", "kernel": f"Q4_0 gate|up GEMM + SwiGLU m={B} (qgemm_xs_kernel, EPI=1)",
                           "achieved": round(gemm_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                           "frac": round(gemm_gbs / HBM_PEAK_GBS, 4), "bytes_per_launch": gemm_bytes,

@@ -80,9 +80,9 @@ __device__ __forceinline__ float rows_sum4(const float (&v)[4]) {
 
 // 8 wavefronts of 32-token steps measured best on MI355X at config 4 (batch 32,
 // 2048 tokens), against 64-token steps, 16 wavefronts of 16 tokens and a
-// double-buffered pipeline.  A pure streaming read peaks at ~6.2 TB/s on this part;
+// double-buffered pipeline.  A long streaming read peaks at ~7.0 TB/s on this part;
 // a loads-only copy of this kernel's access pattern (same grid, pages and per-lane
-// addresses) reaches ~5.5 TB/s, and the kernel about 88% of that.
+// addresses) takes 47.4 us at config 4 (5.7 TB/s), and the kernel 50.0 us.
 constexpr int kTiles = 2;             // 16-token MFMA tiles per wavefront step
 constexpr int kBlock = 16 * kTiles;   // tokens per wavefront step
 constexpr int kWaves = 8;             // wavefronts per workgroup (fp16 path)
@@ -511,11 +511,47 @@ __global__ __launch_bounds__(64) void attn_chunk_generic(
 
 // ----------------------------------------------------------------------------
 // Merge S partials of one (row, head): out = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s.
+// Latency-bound (a few KiB per workgroup), so no load waits for another: thread s
+// reads split s's (m, l), the weights 2^(m_s - M) go through LDS, and each output
+// element's S partials are loaded 8 at a time before they are summed.  Sums run in
+// split order, as the serial form for S > kMergeFast does.
+constexpr int kMergeFast = 128;
 template <typename T>
 __global__ __launch_bounds__(128) void attn_merge(const float* __restrict__ part_o, const float* __restrict__ part_ml,
                                                   T* __restrict__ out, int Hq, int D, int S) {
   const int head = blockIdx.x, row = blockIdx.y;
   const float* ml = part_ml + ((size_t)row * Hq + head) * S * 2;
+  if (S <= kMergeFast) {
+    __shared__ float sw[kMergeFast], sl[kMergeFast], smax[2];
+    const int t = threadIdx.x;
+    const float mv = t < S ? ml[2 * t] : -INFINITY;
+    const float lv = t < S ? ml[2 * t + 1] : 0.f;
+    const float wm = wave_max(mv);
+    if ((t & 63) == 0) smax[t >> 6] = wm;
+    __syncthreads();
+    const float M = fmaxf(smax[0], smax[1]);
+    sw[t] = (t < S && M != -INFINITY) ? exp2f(mv - M) : 0.f;
+    sl[t] = lv;
+    __syncthreads();
+    float den = 0.f;
+    if (M != -INFINITY)
+      for (int s = 0; s < S; ++s) den = fmaf(sl[s], sw[s], den);
+    const float inv = den > 0.f ? 1.f / den : 0.f;
+    const float* po = part_o + ((size_t)row * Hq + head) * S * D;
+    for (int d = t; d < D; d += 128) {
+      float o = 0.f;
+      for (int s0 = 0; s0 < S; s0 += 8) {
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = po[(size_t)min(s0 + j, S - 1) * D + d];
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          if (s0 + j < S) o = fmaf(v[j], sw[s0 + j], o);
+      }
+      out[((size_t)row * Hq + head) * D + d] = from_f32<T>(o * inv);
+    }
+    return;
+  }
   float M = -INFINITY;
   for (int s = 0; s < S; ++s) M = fmaxf(M, ml[2 * s]);
   float den = 0.f;

@@ -61,6 +61,22 @@ def test_attention_fp16_mfma_ragged(device, hq, hkv):
     close16(out.float().cpu().numpy(), ref)
 
 
+@pytest.mark.parametrize("ctx", [[1500, 40, 1], [1024, 1023], [17000, 900, 3]])
+def test_attention_fp32_many_partials(device, ctx):
+    """fp32 pools run 128-token chunks, one partial each: 12 and 8 partials take the merge's
+    batched loads (the first with a last group of 4), 133 partials its serial form."""
+    from cacheir_amd import kernels
+
+    rng = np.random.default_rng(len(ctx) + ctx[0])
+    hq, hkv, d = 4, 2, 64
+    kp, vp, pt, lens = paged.build_pool(rng, ctx, hkv, d, 16, dtype=np.float32)
+    q = rng.standard_normal((len(ctx), hq, d)).astype(np.float32)
+    out = kernels.paged_decode_attention(to_dev(q, device), to_dev(kp, device), to_dev(vp, device), to_dev(pt, device),
+                                         to_dev(lens, device), check_tables=True)
+    ref = paged.paged_attention(q, kp, vp, pt, lens, hq, hkv)
+    np.testing.assert_allclose(out.cpu().numpy(), ref, atol=1e-4, rtol=1e-4)
+
+
 def test_attention_empty_sequence_gives_zeros(device):
     from cacheir_amd import kernels
 

@@ -23,8 +23,9 @@ layers' KV so the 256 MB MALL cannot hold it), the same kernel at BASELINE confi
 (ragged contexts over randomly permuted pages; config 5 with a shared 1024-token prefix, its
 bytes counted once), the same for the largest projection (the
 fused gate|up Q4_0 GEMM + SwiGLU at m = batch, rotated
-over the 32 layers' weights), the same for the dequant GEMV at m = 1 and 8 (BASELINE
-config 3's 14336 -> 4096 projection, rotated over the layers' down weights), the batched GEMM
+over the 32 layers' weights), the same for the dequant GEMV at m = 1, 8 and 32 (BASELINE
+config 3's 14336 -> 4096 and 4096 -> 14336 projections, rotated over the layers' down and gate weights; m = 32
+takes the MFMA GEMM), the batched GEMM
 on MFMA (BASELINE config 5's Q8_0 gate|up + SwiGLU at batch 128: TFLOP/s against the dense fp16
 MFMA peak), the same decode
 step at batch 1 (decode_batch1: the projections and greedy head then run the GEMV), and a CPU
@@ -318,20 +319,29 @@ def main() -> int:
     gemm_gbs = gemm_bytes / (gemm_us * 1e-6) / 1e9
     log(f"gate|up GEMM + SwiGLU {gemm_us:.2f} us/launch (m={B}), {gemm_gbs:.0f} GB/s")
 
-    # ---- the dequant GEMV (m <= 8): BASELINE config 3's 14336 -> 4096 projection, on the layers' down weights ----
+    # ---- the Q4_0 projections 14336 -> 4096 (the layers' down weights) and 4096 -> 14336 (16
+    # layers' gate weights, tiled on their own) at m = 1 and 8 (the dequant GEMV) and m = 32 (the MFMA GEMM) ----
     dn = [base.weights.matmul_weight((f"layer{i}_down_w",)) for i in range(cfg.num_layers)]
+    gt = [base.weights.matmul_weight((f"layer{i}_gate_w",)) for i in range(min(16, cfg.num_layers))]
     gemv = []
-    for m in (1, 8):
-        xv = torch.randn((m, dn[0].k), device=dev, dtype=torch.float16)
-        sp = kernels.choose_splits(m, dn[0].n, dn[0].k)
-        pv = torch.empty((sp, m, dn[0].n), device=dev)
-        us = graph_us_per_launch(lambda it: kernels.qgemm_partial(xv, dn[it % len(dn)], splits=sp, out=pv),
-                                 args.gemm_iters)
-        by = dn[0].nbytes + 2 * m * dn[0].k + 4 * m * dn[0].n  # weights, x, y once
-        gbs = by / (us * 1e-6) / 1e9
-        gemv.append({"m": m, "n": dn[0].n, "k": dn[0].k, "splits": sp, "us_per_launch": round(us, 3),
-                     "bytes_per_launch": by, "achieved": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)})
-        log(f"GEMV m={m} {dn[0].n}x{dn[0].k} {us:.2f} us/launch, {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%} of peak)")
+    for shape, ws_ in (("down", dn), ("gate", gt)):
+        n3, k3 = ws_[0].n, ws_[0].k
+        for m in (1, 8, 32):
+            xv = torch.randn((m, k3), device=dev, dtype=torch.float16)
+            sp = kernels.choose_splits(m, n3, k3)
+            pv = torch.empty((sp, m, n3), device=dev)
+            us = graph_us_per_launch(lambda it: kernels.qgemm_partial(xv, ws_[it % len(ws_)], splits=sp, out=pv),
+                                     args.gemm_iters)
+            by = ws_[0].nbytes + 2 * m * k3 + 4 * m * n3  # weights, x, y once
+            gbs = by / (us * 1e-6) / 1e9
+            row = {"shape": shape, "m": m, "n": n3, "k": k3, "splits": sp,
+                   "kernel": "qgemv_kernel" if m <= 8 else "qgemm_xs_kernel (MFMA)", "us_per_launch": round(us, 3),
+                   "bytes_per_launch": by, "achieved": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+            if m > 8:
+                row["tflops"] = round(2.0 * m * n3 * k3 / (us * 1e-6) / 1e12, 1)
+            gemv.append(row)
+            log(f"{row['kernel']} m={m} {n3}x{k3} {us:.2f} us/launch, {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%} of peak)")
+    del gt
 
     # ---- the batched GEMM on MFMA: BASELINE config 5's gate|up (Qwen2-7B, Q8_0) + SwiGLU at batch 128 ----
     n5, k5, m5 = 2 * 18944, 3584, 128
@@ -414,7 +424,8 @@ def main() -> int:
                           "achieved": round(gemm_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                           "frac": round(gemm_gbs / HBM_PEAK_GBS, 4), "bytes_per_launch": gemm_bytes,
                           "us_per_launch": round(gemm_us, 3)},
-        "roofline_gemv": {"bound": "hbm", "kernel": "Q4_0 dequant GEMV (qgemv_kernel), BASELINE config 3 down shape",
+        "roofline_gemv": {"bound": "hbm", "kernel": "Q4_0 projections, BASELINE config 3 (n x k, y = x W^T): dequant "
+                                                    "GEMV at m <= 8, MFMA GEMM at m = 32",
                           "peak": HBM_PEAK_GBS, "unit": "GB/s", "shapes": gemv},
         "roofline_batched_gemm": {"bound": "mfma",
                                   "kernel": "Q8_0 gate|up GEMM + SwiGLU m=128 (qgemm_xl_kernel, EPI=1), "

@@ -1191,7 +1191,21 @@ __global__ __launch_bounds__(256) void argmax_cand_kernel(const float* __restric
   int bi = 0x7fffffff;
   const float* cv = cand_v + (size_t)m * W;
   const int* ci = cand_i + (size_t)m * W;
-  for (int w = threadIdx.x; w < W; w += 256) argmax_better(bv, bi, cv[w], ci[w]);
+  // 8 candidates per thread in flight at a time: the loop is latency-bound otherwise
+  // (one L2 round trip per candidate; 4008 per row for a 128256-column head).
+  constexpr int U = 8;
+  for (int w0 = threadIdx.x; w0 < W; w0 += 256 * U) {
+    float v[U];
+    int ix[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int w = w0 + 256 * u;
+      v[u] = w < W ? cv[w] : -INFINITY;
+      ix[u] = w < W ? ci[w] : 0x7fffffff;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) argmax_better(bv, bi, v[u], ix[u]);
+  }
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) {
     const float ov = __shfl_xor(bv, off, 64);

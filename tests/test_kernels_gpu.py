@@ -364,6 +364,37 @@ def test_qgemm_swiglu_matches_gemm_then_epilogue(device, fmt, m, k):
     assert np.all(err <= 0), err.max()
 
 
+@pytest.mark.gpu
+@pytest.mark.parametrize("proj,n,k", [("qkv", 4608, 3584), ("down", 3584, 18944), ("gate_up", 18944, 3584)])
+def test_config5_projections_full_size(device, proj, n, k):
+    """BASELINE config 5's Q8_0 projections at batch 128, full Qwen2-7B shapes: QKV (the large-m kernel), down
+    (n spans 28 column groups: the m <= 32 kernel in four row blocks) and gate|up with the fused SwiGLU, against the
+    dequantized oracle.  Scales are |N(0, 5e-4)| so that int8 codes give weights of config 3's size (RMS ~0.03);
+    with config 3's 0.01, |g| and |u| reach ~150 and fp32 accumulation alone moves silu(g) * u by ~2e-3."""
+    from cacheir_amd import kernels
+
+    rng = np.random.default_rng(13)
+    m = 128
+    code = kernels.FMT_NAMES["q8_0"]
+    x = rng.standard_normal((m, k)).astype(np.float16)
+    xd = to_dev(x, device)
+    xf = x.astype(np.float32)
+    if proj != "gate_up":
+        blocks = quant.random_q8_0(rng, n, k, scale_sigma=5e-4)[0]
+        w = kernels.QWeight.from_blocks(to_dev(blocks.reshape(-1), device), code, n, k)
+        got = kernels.qgemm_partial(xd, w).sum(0).cpu().numpy()
+        close16(got, ops.matmul(xf, quant.decode_q8_0(blocks, k)))
+        return
+    gate, up = quant.random_q8_0(rng, n, k, scale_sigma=5e-4)[0], quant.random_q8_0(rng, n, k, scale_sigma=5e-4)[0]
+    w_il = kernels.QWeight.from_blocks(kernels.interleave_gate_up(to_dev(gate, device), to_dev(up, device), n)
+                                       .reshape(-1), code, 2 * n, k)
+    got = kernels.qgemm_swiglu(xd, w_il, torch.float16).float().cpu().numpy()
+    x64 = x.astype(np.float64)
+    g = ops.matmul(x64, quant.decode_q8_0(gate, k).astype(np.float64))
+    u = ops.matmul(x64, quant.decode_q8_0(up, k).astype(np.float64))
+    close16(got, g / (1.0 + np.exp(-g)) * u)
+
+
 def _shared_prefix_case(device, rng, batch, prefix_pages, suffix_lo, suffix_hi, hkv=4, d=128, psize=16):
     """BASELINE config 5 layout: every sequence's first ``prefix_pages`` pages are the same slots; suffix pages
     are distinct and permuted.  Returns pools (torch fp16), page table, lengths and the slot count."""

@@ -96,8 +96,9 @@ def llama3_8b(layers: int):
                        max_position_embeddings=8192, rope_theta=500000.0, rms_norm_eps=1e-5, dtype="float16")
 
 
-def graph_us_per_launch(launch, iters: int, replays: int = 3) -> float:
-    """GPU time per launch of ``launch(i)``: ``iters`` launches captured in one HIP graph, replayed ``replays`` times
+def graph_us_per_launch(launch, iters: int, replays: int = 3, warm_replays: int = 2) -> float:
+    """GPU time per launch of ``launch(i)``: ``iters`` launches captured in one HIP graph, replayed ``warm_replays``
+    times untimed (the first replays after a pause run ~2-4% slow while the clocks come up), then ``replays`` times
     between HIP events on the launch stream (no host launch gaps inside the timed region)."""
     import torch
 
@@ -113,7 +114,8 @@ def graph_us_per_launch(launch, iters: int, replays: int = 3) -> float:
     with torch.cuda.graph(graph):
         for i in range(iters):
             launch(i)
-    graph.replay()
+    for _ in range(warm_replays):
+        graph.replay()
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)

@@ -288,6 +288,12 @@ def main() -> int:
     torch.cuda.synchronize()
     assert torch.equal(plan.next_ids, want), "fused greedy head disagrees with argmax(logits)"
 
+    # Bytes a step must move: every linear weight and norm once, the embedding rows of
+    # the batch only (the table itself is never streamed), and every layer's K/V.  Taken
+    # before the roofline loops below tile extra weight copies into the same store.
+    embed = base.weights.dense("tok_embeddings", torch.float16)
+    weight_bytes = base.weights.nbytes() - embed.numel() * embed.element_size() + B * cfg.hidden_size * 2
+
     ms_step = time_greedy_steps(plan, args.steps, args.warmup)
     toks = B * 1000.0 / ms_step
     assert bool(((plan.next_ids >= 0) & (plan.next_ids < cfg.vocab_size)).all().item()), "ids out of range"
@@ -393,10 +399,6 @@ def main() -> int:
         cpu = cbase.time_decode_step(batch=B, ctx=ctx, hidden=4096, ffn=14336, heads=H, kv_heads=Hkv, vocab=128256,
                                      layers=cfg.num_layers, budget_s=12.0, log=log)
 
-    # Bytes a step must move: every linear weight and norm once, the embedding rows of
-    # the batch only (the table itself is never streamed), and every layer's K/V.
-    embed = base.weights.dense("tok_embeddings", torch.float16)
-    weight_bytes = base.weights.nbytes() - embed.numel() * embed.element_size() + B * cfg.hidden_size * 2
     line = {
         "metric": "decode tokens/s, batch 32, Llama-3-8B-shape Q4_0; paged-attn HBM GB/s",
         "value": round(toks, 2),

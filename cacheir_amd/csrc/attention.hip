@@ -586,7 +586,8 @@ int choose_splits(int rows, int Hkv, int max_context) {
 int launch_attention(const void* q, const void* k_pool, const void* v_pool, const int32_t* page_table,
                      const int32_t* seq_lens, void* out, void* workspace, size_t workspace_bytes,
                      int batch, int q_len, int Hq, int Hkv, int D, int P, int max_pages, float scale,
-                     int kv_dtype, void* stream, QkvIn qkv = QkvIn{nullptr, 0, nullptr, nullptr}) {
+                     int kv_dtype, void* stream, QkvIn qkv = QkvIn{nullptr, 0, nullptr, nullptr},
+                     bool merge = true) {
   CIR_CHECK_ARG(batch >= 0 && q_len >= 1, "attention: batch must be >= 0 and q_len >= 1");
   if (batch == 0) return 0;
   CIR_CHECK_ARG((q || qkv.part) && k_pool && v_pool && page_table && seq_lens && out, "attention: null pointer");
@@ -608,6 +609,7 @@ int launch_attention(const void* q, const void* k_pool, const void* v_pool, cons
                 "attention: the fused QKV input needs decode (q_len 1), fp16 pools, head_dim 128, page_size %% 16 == 0, "
                 "num_heads/num_kv_heads <= 8 and inv_freq/positions");
   const int S = mfma ? choose_splits(rows, Hkv, max_ctx) : generic_chunks(max_ctx);
+  CIR_CHECK_ARG(merge || (mfma && S > 1), "attention: unmerged partials need the fp16 decode path with > 1 split");
   float* part_o = static_cast<float*>(workspace);
   float* part_ml = part_o + (size_t)rows * Hq * S * D;
   dim3 grid(S, Hkv, rows);
@@ -627,7 +629,7 @@ int launch_attention(const void* q, const void* k_pool, const void* v_pool, cons
     }
 #undef CIR_ATT_CASE
     const int st = launch_status();
-    if (st || S == 1) return st;
+    if (st || S == 1 || !merge) return st;
   } else {
     if (kv_dtype == CIR_F16) {
       attn_chunk_generic<f16><<<grid, 64, 0, s>>>(static_cast<const f16*>(q), static_cast<const f16*>(k_pool),
@@ -670,6 +672,15 @@ extern "C" int cir_paged_decode_attention(const void* q, const void* k_pool, con
                                num_heads, num_kv_heads, head_dim, page_size, max_pages, scale, kv_dtype, stream);
 }
 
+extern "C" int cir_paged_decode_splits(int batch, int num_heads, int num_kv_heads, int head_dim, int page_size,
+                                       int max_pages, int kv_dtype) {
+  if (batch <= 0 || num_heads <= 0 || num_kv_heads <= 0 || page_size <= 0 || max_pages <= 0) return 0;
+  const bool mfma = kv_dtype == CIR_F16 && head_dim == 128 && page_size % 16 == 0 && num_heads % num_kv_heads == 0 &&
+                    num_heads / num_kv_heads <= 8;
+  const int ctx = max_pages * page_size;
+  return mfma ? cir::choose_splits(batch, num_kv_heads, ctx) : cir::generic_chunks(ctx);
+}
+
 extern "C" int cir_paged_prefill_attention(const void* q, const void* k_pool, const void* v_pool,
                                            const int32_t* page_table, const int32_t* seq_lens, void* out,
                                            void* workspace, size_t workspace_bytes, int batch, int q_len,
@@ -690,5 +701,18 @@ extern "C" int cir_paged_decode_attention_qkv(const float* qkv_partial, int spli
   return cir::launch_attention(nullptr, k_pool, v_pool, page_table, seq_lens, out, workspace, workspace_bytes, batch,
                                1, num_heads, num_kv_heads, head_dim, page_size, max_pages, scale, CIR_F16, stream,
                                cir::QkvIn{qkv_partial, splits, inv_freq, positions});
+}
+
+extern "C" int cir_paged_decode_attention_qkv_parts(const float* qkv_partial, int splits, const float* inv_freq,
+                                                    const int32_t* positions, void* k_pool, void* v_pool,
+                                                    const int32_t* page_table, const int32_t* seq_lens, void* workspace,
+                                                    size_t workspace_bytes, int batch, int num_heads, int num_kv_heads,
+                                                    int head_dim, int page_size, int max_pages, float scale,
+                                                    void* stream) {
+  CIR_CHECK_ARG(batch == 0 || qkv_partial, "attention_qkv_parts: null qkv_partial");
+  // `out` is never written on this path; the workspace pointer stands in for the non-null check.
+  return cir::launch_attention(nullptr, k_pool, v_pool, page_table, seq_lens, workspace, workspace, workspace_bytes,
+                               batch, 1, num_heads, num_kv_heads, head_dim, page_size, max_pages, scale, CIR_F16,
+                               stream, cir::QkvIn{qkv_partial, splits, inv_freq, positions}, false);
 }
 

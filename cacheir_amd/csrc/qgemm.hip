@@ -843,14 +843,70 @@ constexpr int kGemvMaxWaves = 16;
 // (The fused SwiGLU stays on the GEMM kernel at every m: gate/up tiles must be
 // consumed in pairs, and no GEMV geometry of pairs beat the GEMM's two-tile stages,
 // 21.4 us against 19.2 at m = 1 for the Llama-3-8B gate|up.)
-template <int FMT, int MR, int DW, int XC, int EPI = 0, typename TO = float>
+// Split decode-attention partials as a GEMV input (XM): per (row, head) S <= 8 partial
+// outputs O_s [128] and (max, sum) pairs, laid out as the attention kernel writes them.
+struct AttnParts {
+  const float* o;   // [rows][heads][S][128]
+  const float* ml;  // [rows][heads][S][2]
+  int S, heads;
+};
+constexpr int kAttnMaxParts = 8;
+
+// 8 consecutive head dims (d0..d0+7) of one (row, head) of the merged attention output,
+// rounded to fp16 with the arithmetic and order of attn_merge (attention.hip).  About
+// one value in 16k still rounds one fp16 ulp away from the stored attention output.
+// All loads are issued first.
+__device__ __forceinline__ u32x4 attn_merged_chunk(const AttnParts& a, int row, int head, int d0) {
+  const float* ml = a.ml + ((size_t)row * a.heads + head) * a.S * 2;
+  const float* po = a.o + ((size_t)row * a.heads + head) * a.S * 128 + d0;
+  float2 mv[kAttnMaxParts];
+  float4 o0[kAttnMaxParts], o1[kAttnMaxParts];
+#pragma unroll
+  for (int s = 0; s < kAttnMaxParts; ++s) {
+    const int ss = s < a.S ? s : 0;
+    mv[s] = *reinterpret_cast<const float2*>(ml + 2 * ss);
+    o0[s] = *reinterpret_cast<const float4*>(po + (size_t)ss * 128);
+    o1[s] = *reinterpret_cast<const float4*>(po + (size_t)ss * 128 + 4);
+  }
+  float M = -INFINITY;
+#pragma unroll
+  for (int s = 0; s < kAttnMaxParts; ++s)
+    if (s < a.S) M = fmaxf(M, mv[s].x);
+  float w[kAttnMaxParts];
+#pragma unroll
+  for (int s = 0; s < kAttnMaxParts; ++s) w[s] = (s < a.S && M != -INFINITY) ? exp2f(mv[s].x - M) : 0.f;
+  float den = 0.f;
+  if (M != -INFINITY)
+#pragma unroll
+    for (int s = 0; s < kAttnMaxParts; ++s)
+      if (s < a.S) den = fmaf(mv[s].y, w[s], den);
+  const float inv = den > 0.f ? 1.f / den : 0.f;
+  float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < kAttnMaxParts; ++s)
+    if (s < a.S) {
+      const float v[8] = {o0[s].x, o0[s].y, o0[s].z, o0[s].w, o1[s].x, o1[s].y, o1[s].z, o1[s].w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = fmaf(v[e], w[s], o[e]);
+    }
+  uint32_t h[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const f16x2 two = {static_cast<f16>(o[2 * e] * inv), static_cast<f16>(o[2 * e + 1] * inv)};
+    h[e] = __builtin_bit_cast(uint32_t, two);
+  }
+  return u32x4{h[0], h[1], h[2], h[3]};
+}
+
+template <int FMT, int MR, int DW, int XC, int EPI = 0, typename TO = float, bool XM = false>
 __global__ __launch_bounds__(64 * kGemvMaxWaves) void qgemv_kernel(const f16* __restrict__ x, int ldx,
                                                                  const uint8_t* __restrict__ wq,
                                                                  const uint16_t* __restrict__ wd,
                                                                  float* __restrict__ part, int M, int N, int K,
                                                                  int nq, int tpw, TO* __restrict__ out = nullptr,
-                                                                 int TW = 0) {
+                                                                 int TW = 0, AttnParts ap = AttnParts{}) {
   static_assert(EPI == 0 || EPI == 2, "GEMV epilogues: partials or argmax candidates");
+  static_assert(!XM || (EPI == 0 && !is_row_fmt(FMT)), "attention-partials input: block formats, partials out");
   static_assert(EPI == 0 || !is_row_fmt(FMT), "row formats scale after the loop: EPI 0 only");
   constexpr int LB = Stage<FMT, 1, 1>::LB;
   extern __shared__ __align__(16) uint8_t xs[];
@@ -881,7 +937,10 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void qgemv_kernel(const f16* __
     for (int u = 0; u < XC; ++u) {
       const bool past = r >= M;
       const int rr = past ? M - 1 : r, cc = past ? cols16 - 1 : col;
-      xv[u] = *reinterpret_cast<const u32x4*>(x + (size_t)rr * ldx + 128 * q0 + 8 * cc);
+      if constexpr (XM)  // quad q of k is head q (head_dim 128)
+        xv[u] = attn_merged_chunk(ap, rr, q0 + (cc >> 4), 8 * (cc & 15));
+      else
+        xv[u] = *reinterpret_cast<const u32x4*>(x + (size_t)rr * ldx + 128 * q0 + 8 * cc);
       xoff[u] = rr * rs + 16 * (cc ^ (rr & 7));
       r += r_step;
       col += c_step;
@@ -1107,9 +1166,9 @@ int gemv_splits(int m, int n, int k) {
 // One GEMV launch: EPI 0 (partials into part) or 2 (argmax candidates into part /
 // out, one split).  Returns the number of wavefronts that own tiles (the candidate
 // count per row for EPI 2).
-template <int FMT, int EPI, typename TO = float>
+template <int FMT, int EPI, typename TO = float, bool XM = false>
 int launch_qgemv(const f16* x, int ldx, const uint8_t* wq, const uint16_t* wd, float* part, int M, int N, int K,
-                 int splits, hipStream_t s, TO* out = nullptr) {
+                 int splits, hipStream_t s, TO* out = nullptr, AttnParts ap = AttnParts{}) {
   const int NTILES = (N + 15) / 16;
   const int nq = (K / 128) / splits;
   GemvGeom g = gemv_geometry(M, N, K, splits);
@@ -1119,8 +1178,8 @@ int launch_qgemv(const f16* x, int ldx, const uint8_t* wq, const uint16_t* wd, f
   const size_t lds = (size_t)M * 256 * nq;
   const int xc_need = (16 * M * nq + 64 * g.waves - 1) / (64 * g.waves);
   auto go = [&]<int MR, int XC>() {
-    qgemv_kernel<FMT, MR, CIR_GV_DW, XC, EPI, TO>
-        <<<grid, 64 * g.waves, lds, s>>>(x, ldx, wq, wd, part, M, N, K, nq, g.tpw, out, waves_per_split);
+    qgemv_kernel<FMT, MR, CIR_GV_DW, XC, EPI, TO, XM>
+        <<<grid, 64 * g.waves, lds, s>>>(x, ldx, wq, wd, part, M, N, K, nq, g.tpw, out, waves_per_split, ap);
   };
   auto by_xc = [&]<int MR>() {
     if (xc_need <= 1) go.template operator()<MR, 1>();
@@ -1437,6 +1496,32 @@ extern "C" int cir_qgemm(const void* x, int ldx, const void* w_tiled, int fmt, f
   } else {
     dispatch_qgemm<CIR_I8_ROW>(xh, ldx, q, d, y_partial, m, n, k, splits, s);
   }
+  return launch_status();
+}
+
+extern "C" int cir_qgemm_attn(const float* attn_part_o, const float* attn_part_ml, int attn_splits, int num_heads,
+                              const void* w_tiled, int fmt, float* y_partial, int m, int n, int k, int splits,
+                              void* stream) {
+  CIR_CHECK_ARG(fmt == CIR_Q4_0 || fmt == CIR_Q8_0, "qgemm_attn: block formats only (got %d)", fmt);
+  CIR_CHECK_ARG(m >= 0 && n >= 0 && num_heads > 0, "qgemm_attn: bad sizes");
+  if (m == 0 || n == 0) return 0;
+  CIR_CHECK_ARG(k == num_heads * 128, "qgemm_attn: k (%d) must be num_heads (%d) x 128", k, num_heads);
+  CIR_CHECK_ARG(attn_splits >= 1 && attn_splits <= cir::kAttnMaxParts, "qgemm_attn: attn_splits %d out of 1..%d",
+                attn_splits, cir::kAttnMaxParts);
+  CIR_CHECK_ARG(splits >= 1 && (k / 128) % splits == 0, "qgemm_attn: splits (%d) must divide k/128 (%d)", splits,
+                k / 128);
+  CIR_CHECK_ARG(cir::gemv_fits(m, k, splits), "qgemm_attn: m %d with %d quads per split exceeds the GEMV stage", m,
+                (k / 128) / splits);
+  CIR_CHECK_ARG(attn_part_o && attn_part_ml && w_tiled && y_partial, "qgemm_attn: null pointer");
+  const size_t tiles = (size_t)((n + 15) / 16) * (k / 128);
+  const uint8_t* q = static_cast<const uint8_t*>(w_tiled);
+  const uint16_t* d = reinterpret_cast<const uint16_t*>(q + tiles * 64 * quant_bytes_per_lane(fmt));
+  const cir::AttnParts ap{attn_part_o, attn_part_ml, attn_splits, num_heads};
+  hipStream_t s = as_stream(stream);
+  if (fmt == CIR_Q4_0)
+    cir::launch_qgemv<CIR_Q4_0, 0, float, true>(nullptr, k, q, d, y_partial, m, n, k, splits, s, nullptr, ap);
+  else
+    cir::launch_qgemv<CIR_Q8_0, 0, float, true>(nullptr, k, q, d, y_partial, m, n, k, splits, s, nullptr, ap);
   return launch_status();
 }
 

@@ -36,6 +36,9 @@ _SIGNATURES = {
                                             _c_int, _c_int, _c_float, _c_int, _vp]),
     "cir_paged_decode_attention_qkv": (_c_int, [_vp, _c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_size, _c_int,
                                                 _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _vp]),
+    "cir_paged_decode_splits": (_c_int, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int]),
+    "cir_paged_decode_attention_qkv_parts": (_c_int, [_vp, _c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_size, _c_int,
+                                                      _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _vp]),
     "cir_paged_prefill_attention": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_size, _c_int, _c_int, _c_int, _c_int,
                                              _c_int, _c_int, _c_int, _c_float, _c_int, _vp]),
     "cir_qweight_tiled_bytes": (_c_size, [_c_int, _c_int, _c_int]),
@@ -45,6 +48,7 @@ _SIGNATURES = {
     "cir_qgemm_splits": (_c_int, [_c_int, _c_int, _c_int]),
     "cir_qgemm_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int]),
     "cir_qgemm": (_c_int, [_vp, _c_int, _vp, _c_int, _vp, _c_int, _c_int, _c_int, _c_int, _vp]),
+    "cir_qgemm_attn": (_c_int, [_vp, _vp, _c_int, _c_int, _vp, _c_int, _vp, _c_int, _c_int, _c_int, _c_int, _vp]),
     "cir_qgemm_swiglu": (_c_int, [_vp, _c_int, _vp, _c_int, _vp, _c_int, _c_int, _c_int, _c_int, _vp]),
     "cir_qgemm_argmax_workspace_bytes": (_c_size, [_c_int, _c_int]),
     "cir_qgemm_argmax": (_c_int, [_vp, _c_int, _vp, _c_int, _vp, _vp, _c_size, _c_int, _c_int, _c_int, _vp]),

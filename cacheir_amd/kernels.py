@@ -193,6 +193,59 @@ def dequant_tiled(w: QWeight) -> torch.Tensor:
     return out
 
 
+def paged_decode_splits(batch: int, num_heads: int, num_kv_heads: int, head_dim: int, page_size: int,
+                        max_pages: int, kv_dtype: torch.dtype) -> int:
+    """Context splits the decode attention uses at these sizes (``cir_paged_decode_splits``)."""
+    return hip.load().cir_paged_decode_splits(batch, num_heads, num_kv_heads, head_dim, page_size, max_pages,
+                                              hip.dtype_code(kv_dtype))
+
+
+def paged_decode_attention_qkv_parts(part, inv_freq, positions, k_pool, v_pool, page_table, seq_lens, *,
+                                     num_heads: int, workspace: torch.Tensor, scale: float | None = None) -> int:
+    """``paged_decode_attention_qkv`` without the merge: the split partials stay in ``workspace`` (O
+    ``[B, Hq, S, D]`` fp32 at its start, (max, sum) ``[B, Hq, S, 2]`` after it) for ``qgemm_attn``.
+    Returns S (> 1 is required)."""
+    _cuda(part, "part")
+    _req(part.dtype == torch.float32 and part.dim() == 3, "part must be float32 [splits, batch, n]", TypeError)
+    splits, batch, n = part.shape
+    _req(k_pool.dtype == torch.float16, "the fused QKV attention needs float16 pools", TypeError)
+    _, kvh, psize, hd = _check_pool(k_pool, k_pool, v_pool, page_table, seq_lens, num_heads, False)
+    _req(n == (num_heads + 2 * kvh) * hd, "qkv partial width must be (num_heads + 2 kv_heads) * head_dim")
+    _req(page_table.shape[0] == batch and seq_lens.shape == (batch,), "shape mismatch")
+    _cuda(positions, "positions")
+    _cuda(inv_freq, "inv_freq")
+    _cuda(workspace, "workspace")
+    max_pages = page_table.shape[1]
+    S = paged_decode_splits(batch, num_heads, kvh, hd, psize, max_pages, k_pool.dtype)
+    _req(S > 1, "the unmerged decode attention needs more than one context split")
+    scale = 1.0 / math.sqrt(hd) if scale is None else scale
+    hip.call("cir_paged_decode_attention_qkv_parts", part.data_ptr(), splits, inv_freq.data_ptr(),
+             positions.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(), page_table.data_ptr(), seq_lens.data_ptr(),
+             workspace.data_ptr(), workspace.numel() * workspace.element_size(), batch, num_heads, kvh, hd, psize,
+             max_pages, float(scale), hip.stream_handle())
+    return S
+
+
+def qgemm_attn(workspace: torch.Tensor, attn_splits: int, num_heads: int, w: QWeight, m: int,
+               splits: int | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """fp32 partials ``[splits, m, n]`` of ``merge(attention partials) @ W^T`` (``cir_qgemm_attn``): the attention
+    output of ``m`` rows, merged from ``workspace`` as ``paged_decode_attention_qkv_parts`` left it, is the input."""
+    _cuda(workspace, "workspace")
+    _req(w.k == num_heads * 128, "the O projection's k must be num_heads * 128")
+    head_dim = 128
+    o_floats = m * num_heads * attn_splits * head_dim
+    _req(workspace.numel() * workspace.element_size() >= 4 * (o_floats + m * num_heads * attn_splits * 2),
+         "workspace smaller than the attention partials")
+    splits = choose_splits(m, w.n, w.k) if splits is None else splits
+    if out is None:
+        out = torch.empty((splits, m, w.n), dtype=torch.float32, device=workspace.device)
+    _req(out.numel() >= splits * m * w.n and out.dtype == torch.float32, "partial buffer too small")
+    base = workspace.data_ptr()
+    hip.call("cir_qgemm_attn", base, base + 4 * o_floats, attn_splits, num_heads, w.tiled.data_ptr(), w.fmt,
+             out.data_ptr(), m, w.n, w.k, splits, hip.stream_handle())
+    return out.view(-1)[: splits * m * w.n].view(splits, m, w.n)
+
+
 def choose_splits(m: int, n: int, k: int) -> int:
     """k-split the library tunes ``cir_qgemm`` for at this shape (``cir_qgemm_splits``)."""
     s = hip.load().cir_qgemm_splits(m, n, k)

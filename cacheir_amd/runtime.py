@@ -214,8 +214,19 @@ class StepPlan:
             self.launches.append(lambda t=t, out=out: kernels.cast(t, out.dtype, out=out))
             return out
 
-        def gemm(x: torch.Tensor, weight) -> tuple[Any, int, int]:
-            """Queue the GEMM into the shared workspace; returns (partials getter, splits, n)."""
+        def gemm(x, weight) -> tuple[Any, int, int]:
+            """Queue the GEMM into the shared workspace; returns (partials getter, splits, n).  ``x`` may be the
+            marker of split attention partials left in the attention workspace (merged by the GEMV)."""
+            if isinstance(x, tuple) and x[0] == "attn-parts":
+                _, S, heads = x
+                n, k = weight.n, weight.k
+                splits = kernels.choose_splits(rows, n, k)
+                self._gemm_need = max(self._gemm_need, splits * rows * n)
+                self.launches.append(lambda w=weight, s=splits, S=S, h=heads: kernels.qgemm_attn(
+                    self.attn_ws, S, h, w, rows, splits=s, out=self.gemm_ws))
+                rt._count("rocm.attn_merge_qgemv")
+                part = lambda s=splits, n=n: self.gemm_ws[: s * rows * n].view(s, rows, n)
+                return part, splits, n
             if isinstance(weight, kernels.QWeight):
                 n, k = weight.n, weight.k
                 splits = kernels.choose_splits(rows, n, k)
@@ -281,6 +292,19 @@ class StepPlan:
                 out = buf(heads * hd, rt.dtype)
                 kp, vp = rt.kv_allocator.layer_pools(layer)
                 qin = env[ins[0]]
+                if isinstance(qin, tuple) and qin[0] == "qkv-partials" and self._merge_into_o(
+                        consumers.get(outs[0], []), outs[0], graph, heads, hd, kp):
+                    # the split partials stay in the workspace; the O projection's GEMV merges them
+                    _, part, inv, _ = qin
+                    S = kernels.paged_decode_splits(self.batch, heads, kp.shape[1], hd, kp.shape[2], self.max_pages,
+                                                    kp.dtype)
+                    self.launches.append(lambda part=part, inv=inv, kp=kp, vp=vp, h=heads:
+                                         kernels.paged_decode_attention_qkv_parts(
+                                             part(), inv, self.positions, kp, vp, self.page_table, self.seq_lens,
+                                             num_heads=h, workspace=self.attn_ws))
+                    rt._count("rocm.rope_kv_append_paged_attention_decode_parts")
+                    env[outs[0]] = ("attn-parts", S, heads)
+                    continue
                 if isinstance(qin, tuple) and qin[0] == "qkv-partials":
                     _, part, inv, _ = qin
                     ov = out.view(rows, heads, hd)
@@ -383,6 +407,24 @@ class StepPlan:
             raise NotImplementedError("graph output is not a tensor value")
         self.logits = logits
         self.next_ids = torch.zeros(rows, dtype=torch.int64, device=rt.device)
+
+    def _merge_into_o(self, users: list[Node], value: str, graph: Graph, heads: int, head_dim: int,
+                      k_pool: torch.Tensor) -> bool:
+        """At batch <= 8 a decode attention that splits its context leaves the partials for the O projection's
+        GEMV to merge (``cir_qgemm_attn``) when that projection, a Q4_0/Q8_0 matmul, is the only reader."""
+        if self.rows > 8 or head_dim != 128 or len(users) != 1 or users[0].op not in _MATMUL_OPS:
+            return False
+        if value in graph.outputs or users[0].inputs[0] != value:
+            return False
+        if not self.rt.weights.is_blocked((users[0].inputs[1],)):
+            return False
+        w = self.rt.weights.matmul_weight((users[0].inputs[1],))
+        if not isinstance(w, kernels.QWeight) or w.fmt not in (hip.CIR_Q4_0, hip.CIR_Q8_0) or w.k != heads * 128:
+            return False
+        S = kernels.paged_decode_splits(self.batch, heads, k_pool.shape[1], head_dim, k_pool.shape[2],
+                                        self.max_pages, k_pool.dtype)
+        splits = kernels.choose_splits(self.rows, w.n, w.k)
+        return 1 < S <= 8 and self.rows * (w.k // 128 // splits) <= 256
 
     @staticmethod
     def _normalizer(users: list[Node], value: str) -> Node | None:

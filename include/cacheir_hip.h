@@ -80,6 +80,24 @@ int cir_paged_decode_attention_qkv(const float* qkv_partial, int splits, const f
                                    int num_kv_heads, int head_dim, int page_size, int max_pages,
                                    float scale, void* stream);
 
+/* The number of context splits S the decode attention above uses for these sizes
+ * (1: each workgroup writes the finished output).  No reference counterpart: it tells
+ * a caller whether cir_paged_decode_attention_qkv_parts applies (S > 1). */
+int cir_paged_decode_splits(int batch, int num_heads, int num_kv_heads, int head_dim, int page_size, int max_pages,
+                            int kv_dtype);
+
+/* cir_paged_decode_attention_qkv without its merge: the S > 1 split partials stay in
+ * the workspace, O as float [batch][num_heads][S][head_dim] at its start and (max,
+ * sum) as float [batch][num_heads][S][2] right after, for cir_qgemm_attn to merge
+ * while it stages the O projection's input.  Pool contents as with the merged call.
+ * Same replaced pair as cir_paged_decode_attention_qkv; the merge itself is the last
+ * step of the reference's attention (cacheir/backends/triton_kernels.py:174-217). */
+int cir_paged_decode_attention_qkv_parts(const float* qkv_partial, int splits, const float* inv_freq,
+                                         const int32_t* positions, void* k_pool, void* v_pool,
+                                         const int32_t* page_table, const int32_t* seq_lens, void* workspace,
+                                         size_t workspace_bytes, int batch, int num_heads, int num_kv_heads,
+                                         int head_dim, int page_size, int max_pages, float scale, void* stream);
+
 /* Causal prefill over the same paged pool (reference prefill attention semantics,
  * cacheir/runtime/cpu.py:361-368): q is [batch * q_len, num_heads, head_dim]; row
  * (b, s) attends to tokens t < seq_lens[b] - q_len + s + 1, where seq_lens[b] is the
@@ -135,6 +153,16 @@ size_t cir_qgemm_workspace_bytes(int m, int n, int splits);
  * splits must divide k/128.  Requires k % 128 == 0. */
 int cir_qgemm(const void* x, int ldx, const void* w_tiled, int fmt, float* y_partial,
               int m, int n, int k, int splits, void* stream);
+
+/* The O projection of a decode step fed straight from split attention partials
+ * (cir_paged_decode_attention_qkv_parts): the workgroup merges each head's S <= 8
+ * partials into the fp16 attention output (the arithmetic of the attention's own merge;
+ * about one value in 16k rounds one fp16 ulp apart) while staging its activations,
+ * then runs as cir_qgemm.  Block formats,
+ * k = num_heads * 128, m <= 8 with m * (k/128/splits) <= 256.  Replaces the
+ * attention output -> o_proj quantized matmul pair (cacheir/runtime/cuda.py:932-954). */
+int cir_qgemm_attn(const float* attn_part_o, const float* attn_part_ml, int attn_splits, int num_heads,
+                   const void* w_tiled, int fmt, float* y_partial, int m, int n, int k, int splits, void* stream);
 
 /* Gate|up projection fused with SwiGLU (cacheir/runtime/cpu.py:266-279,
  * cuda.py:859-871 quantized_fused_swiglu): out[m][j] = silu(g) * u with g, u the

@@ -333,6 +333,55 @@ def test_fused_qkv_decode_attention_matches_epilogue_then_attention(device, batc
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
+@pytest.mark.parametrize("batch,hq,hkv,ctx_hi", [(1, 32, 8, 2048), (4, 32, 8, 2048), (8, 32, 8, 1500), (2, 28, 4, 900)])
+def test_o_projection_from_attention_parts_matches_merged_path(device, fmt, batch, hq, hkv, ctx_hi):
+    """cir_paged_decode_attention_qkv_parts + cir_qgemm_attn (the merge inside the O projection's staging) against
+    cir_paged_decode_attention_qkv + cir_qgemm on its output: the appended K/V bitwise; the O partials within the
+    fp16 bound (the merged fp16 attention values agree except for rare one-ulp roundings, about one in 16k)."""
+    from cacheir_amd import kernels
+
+    rng = np.random.default_rng(batch * 31 + hq + (fmt == "q8_0"))
+    d, psize = 128, 16
+    lens = rng.integers(ctx_hi // 2, ctx_hi + 1, batch).astype(np.int32)
+    positions = (lens - 1).astype(np.int32)
+    pages = [-(-int(n) // psize) for n in lens]
+    max_pages = max(pages)
+    slots = sum(pages) + 2
+    perm = rng.permutation(slots).astype(np.int32)
+    pt = np.zeros((batch, max_pages), np.int32)
+    o = 0
+    for b, n in enumerate(pages):
+        pt[b, :n] = perm[o:o + n]
+        o += n
+    part = rng.standard_normal((2, batch, (hq + 2 * hkv) * d)).astype(np.float32)
+    inv = (1.0 / (500000.0 ** (np.arange(0, d // 2, dtype=np.float32) * 2.0 / d))).astype(np.float32)
+    kp0 = torch.randn((slots, hkv, psize, d), device=device).half()
+    vp0 = torch.randn((slots, hkv, psize, d), device=device).half()
+    P, I, POS, PT, L = (to_dev(a, device) for a in (part, inv, positions, pt, lens))
+    S = kernels.paged_decode_splits(batch, hq, hkv, d, psize, max_pages, torch.float16)
+    assert S > 1
+    n = 4096
+    enc = quant.random_q4_0 if fmt == "q4_0" else quant.random_q8_0
+    blocks = enc(rng, n, hq * d)[0]
+    w = kernels.QWeight.from_blocks(to_dev(blocks.reshape(-1), device), kernels.FMT_NAMES[fmt], n, hq * d)
+    splits = kernels.choose_splits(batch, n, hq * d)
+
+    kp1, vp1 = kp0.clone(), vp0.clone()
+    attn = kernels.paged_decode_attention_qkv(P, I, POS, kp1, vp1, PT, L, num_heads=hq)
+    ref = kernels.qgemm_partial(attn.view(batch, hq * d), w, splits=splits)
+
+    kp2, vp2 = kp0.clone(), vp0.clone()
+    ws = kernels.attention_workspace(batch, hq, d, max_pages * psize, device)
+    got_s = kernels.paged_decode_attention_qkv_parts(P, I, POS, kp2, vp2, PT, L, num_heads=hq, workspace=ws)
+    got = kernels.qgemm_attn(ws, got_s, hq, w, batch, splits=splits)
+    torch.cuda.synchronize()
+    assert got_s == S
+    assert torch.equal(kp2, kp1) and torch.equal(vp2, vp1), "appended K/V differ"
+    torch.testing.assert_close(got, ref, rtol=1e-3, atol=2e-3)  # a one-ulp fp16 flip times |w| <= ~1
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
 @pytest.mark.parametrize("m,k", [(1, 512), (8, 512), (32, 512), (48, 512), (128, 640), (1, 4096), (3, 4096),
                                  (8, 4096)])
 def test_qgemm_swiglu_matches_gemm_then_epilogue(device, fmt, m, k):

@@ -35,6 +35,9 @@
 
 #include <math.h>
 
+#include <atomic>
+#include <mutex>
+
 namespace cir {
 namespace {
 
@@ -583,11 +586,28 @@ int choose_splits(int rows, int Hkv, int max_context) {
   return max(1, min(want, max_splits(max_context)));
 }
 
+// The MFMA kernel serves fp16 pools with head_dim 128, pages of a multiple of 16
+// tokens and up to 8 query heads per KV head; everything else runs the generic kernel.
+bool mfma_path(int kv_dtype, int D, int P, int G) { return kv_dtype == CIR_F16 && D == 128 && P % 16 == 0 && G <= 8; }
+
+// Context splits of a launch: about one workgroup per CU on the MFMA path, one
+// partial per 128-token chunk on the generic path.
+int launch_splits(int rows, int Hkv, int max_ctx, bool mfma) {
+  return mfma ? choose_splits(rows, Hkv, max_ctx) : generic_chunks(max_ctx);
+}
+
+// Bytes of split partials (O, then (max, sum)) a launch writes: none when the MFMA
+// kernel runs unsplit and writes the output itself.
+size_t partial_bytes(int rows, int Hq, int D, int S, bool mfma) {
+  if (mfma && S == 1) return 0;
+  return (size_t)rows * Hq * S * ((size_t)D + 2) * sizeof(float);
+}
+
 int launch_attention(const void* q, const void* k_pool, const void* v_pool, const int32_t* page_table,
                      const int32_t* seq_lens, void* out, void* workspace, size_t workspace_bytes,
                      int batch, int q_len, int Hq, int Hkv, int D, int P, int max_pages, float scale,
                      int kv_dtype, void* stream, QkvIn qkv = QkvIn{nullptr, 0, nullptr, nullptr},
-                     bool merge = true) {
+                     bool merge = true, bool exact_workspace = false) {
   CIR_CHECK_ARG(batch >= 0 && q_len >= 1, "attention: batch must be >= 0 and q_len >= 1");
   if (batch == 0) return 0;
   CIR_CHECK_ARG((q || qkv.part) && k_pool && v_pool && page_table && seq_lens && out, "attention: null pointer");
@@ -598,17 +618,20 @@ int launch_attention(const void* q, const void* k_pool, const void* v_pool, cons
   const int rows = batch * q_len;
   const int max_ctx = max_pages * P;
   CIR_CHECK_ARG(rows <= 65535 && Hkv <= 65535, "attention: grid too large");
-  const size_t need = cir_paged_attention_workspace_bytes(rows, Hq, D, max_ctx);
-  CIR_CHECK_ARG(workspace && workspace_bytes >= need, "attention: workspace too small (%zu < %zu)", workspace_bytes,
-                need);
   const float scale_log2 = scale * kLog2e;
   const int G = Hq / Hkv;
   hipStream_t s = as_stream(stream);
-  const bool mfma = kv_dtype == CIR_F16 && D == 128 && P % 16 == 0 && G <= 8;
+  const bool mfma = mfma_path(kv_dtype, D, P, G);
+  const int S = launch_splits(rows, Hkv, max_ctx, mfma);
+  // The advertised size (cir_paged_attention_workspace_bytes) covers any split count;
+  // the static-scratch entry point checks the bytes this launch writes instead.
+  const size_t need = exact_workspace ? partial_bytes(rows, Hq, D, S, mfma)
+                                      : cir_paged_attention_workspace_bytes(rows, Hq, D, max_ctx);
+  CIR_CHECK_ARG(workspace && workspace_bytes >= need, "attention: workspace too small (%zu < %zu)", workspace_bytes,
+                need);
   CIR_CHECK_ARG(!qkv.part || (mfma && q_len == 1 && qkv.splits >= 1 && qkv.inv_freq && qkv.positions),
                 "attention: the fused QKV input needs decode (q_len 1), fp16 pools, head_dim 128, page_size %% 16 == 0, "
                 "num_heads/num_kv_heads <= 8 and inv_freq/positions");
-  const int S = mfma ? choose_splits(rows, Hkv, max_ctx) : generic_chunks(max_ctx);
   CIR_CHECK_ARG(merge || (mfma && S > 1), "attention: unmerged partials need the fp16 decode path with > 1 split");
   float* part_o = static_cast<float*>(workspace);
   float* part_ml = part_o + (size_t)rows * Hq * S * D;
@@ -675,10 +698,9 @@ extern "C" int cir_paged_decode_attention(const void* q, const void* k_pool, con
 extern "C" int cir_paged_decode_splits(int batch, int num_heads, int num_kv_heads, int head_dim, int page_size,
                                        int max_pages, int kv_dtype) {
   if (batch <= 0 || num_heads <= 0 || num_kv_heads <= 0 || page_size <= 0 || max_pages <= 0) return 0;
-  const bool mfma = kv_dtype == CIR_F16 && head_dim == 128 && page_size % 16 == 0 && num_heads % num_kv_heads == 0 &&
-                    num_heads / num_kv_heads <= 8;
-  const int ctx = max_pages * page_size;
-  return mfma ? cir::choose_splits(batch, num_kv_heads, ctx) : cir::generic_chunks(ctx);
+  const bool mfma = num_heads % num_kv_heads == 0 &&
+                    cir::mfma_path(kv_dtype, head_dim, page_size, num_heads / num_kv_heads);
+  return cir::launch_splits(batch, num_kv_heads, max_pages * page_size, mfma);
 }
 
 extern "C" int cir_paged_prefill_attention(const void* q, const void* k_pool, const void* v_pool,
@@ -716,3 +738,80 @@ extern "C" int cir_paged_decode_attention_qkv_parts(const float* qkv_partial, in
                                stream, cir::QkvIn{qkv_partial, splits, inv_freq, positions}, false);
 }
 
+
+// ----------------------------------------------------------------------------
+// Decode attention that allocates nothing (cir_paged_decode_attention_noalloc).
+// The split partials go to `scratch`, a device array of fixed size that every call
+// on a GPU shares.  Host code never passes the array's name to a kernel (on the
+// host it is only a stand-in for the symbol): its device address is looked up once
+// per device with hipGetSymbolAddress and kept in g_scratch_ptr.
+static constexpr size_t kScratchBytes = CIR_ATTENTION_NOALLOC_MAX_BYTES;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace cir {
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch_ptr[kMaxDevices];
+std::mutex g_scratch_mu;
+
+// Device address of `scratch` on the current device (looked up on the first call
+// for that device, with that device current).
+int scratch_on_current_device(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    set_error("attention_noalloc: hipGetDevice failed: %s", hipGetErrorString(e));
+    return static_cast<int>(e);
+  }
+  if (dev < 0 || dev >= kMaxDevices) {
+    set_error("attention_noalloc: device %d beyond the %d devices the library tracks", dev, kMaxDevices);
+    return static_cast<int>(hipErrorInvalidDevice);
+  }
+  void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (!p) {
+      e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || !p) {
+        set_error("attention_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                  hipGetErrorString(e));
+        return static_cast<int>(e != hipSuccess ? e : hipErrorInvalidSymbol);
+      }
+      g_scratch_ptr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return 0;
+}
+
+}  // namespace
+}  // namespace cir
+
+extern "C" int cir_paged_decode_attention_noalloc(const void* q, const void* k_pool, const void* v_pool,
+                                                  const int32_t* page_table, const int32_t* seq_lens, void* out,
+                                                  int batch, int num_heads, int num_kv_heads, int head_dim,
+                                                  int page_size, int max_pages, float scale, int kv_dtype,
+                                                  void* stream) {
+  CIR_CHECK_ARG(batch >= 0, "attention_noalloc: batch must be >= 0");
+  if (batch == 0) return 0;
+  CIR_CHECK_ARG(num_kv_heads > 0 && num_heads > 0 && num_heads % num_kv_heads == 0,
+                "attention_noalloc: num_heads (%d) must be a multiple of num_kv_heads (%d)", num_heads, num_kv_heads);
+  CIR_CHECK_ARG(head_dim > 0 && head_dim <= 256, "attention_noalloc: head_dim %d out of range (1..256)", head_dim);
+  CIR_CHECK_ARG(page_size > 0 && max_pages > 0, "attention_noalloc: page_size and max_pages must be positive");
+  CIR_CHECK_ARG(batch <= 65535, "attention_noalloc: grid too large");
+  const bool mfma = cir::mfma_path(kv_dtype, head_dim, page_size, num_heads / num_kv_heads);
+  const int S = cir::launch_splits(batch, num_kv_heads, max_pages * page_size, mfma);
+  const size_t need = cir::partial_bytes(batch, num_heads, head_dim, S, mfma);
+  CIR_CHECK_ARG(need <= kScratchBytes,
+                "attention_noalloc: the split partials need %zu bytes, more than the %zu bytes of static scratch "
+                "(batch %d, %d heads, head_dim %d, %d splits); use cir_paged_decode_attention with a workspace",
+                need, kScratchBytes, batch, num_heads, head_dim, S);
+  void* ws = nullptr;
+  const int st = cir::scratch_on_current_device(&ws);
+  if (st) return st;
+  return cir::launch_attention(q, k_pool, v_pool, page_table, seq_lens, out, ws, kScratchBytes, batch, 1, num_heads,
+                               num_kv_heads, head_dim, page_size, max_pages, scale, kv_dtype, stream,
+                               cir::QkvIn{nullptr, 0, nullptr, nullptr}, true, true);
+}

@@ -24,6 +24,7 @@ CIR_Q4_0 = 2
 CIR_Q8_0 = 8
 CIR_I4_ROW = 64  # the reference's per-row asymmetric int4 packing
 CIR_I8_ROW = 65  # ... and int8
+ATTENTION_NOALLOC_MAX_BYTES = 16 << 20  # CIR_ATTENTION_NOALLOC_MAX_BYTES
 
 _c_int, _c_size, _c_float, _vp = ctypes.c_int, ctypes.c_size_t, ctypes.c_float, ctypes.c_void_p
 
@@ -34,6 +35,8 @@ _SIGNATURES = {
     "cir_paged_attention_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int, _c_int]),
     "cir_paged_decode_attention": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_size, _c_int, _c_int, _c_int, _c_int,
                                             _c_int, _c_int, _c_float, _c_int, _vp]),
+    "cir_paged_decode_attention_noalloc": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int,
+                                                    _c_int, _c_int, _c_float, _c_int, _vp]),
     "cir_paged_decode_attention_qkv": (_c_int, [_vp, _c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_size, _c_int,
                                                 _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _vp]),
     "cir_paged_decode_splits": (_c_int, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int]),

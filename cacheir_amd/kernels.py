@@ -77,6 +77,25 @@ def paged_decode_attention(q, k_pool, v_pool, page_table, seq_lens, *, scale: fl
     return out
 
 
+def paged_decode_attention_noalloc(q, k_pool, v_pool, page_table, seq_lens, *, scale: float | None = None,
+                                   out: torch.Tensor | None = None) -> torch.Tensor:
+    """``paged_decode_attention`` through ``cir_paged_decode_attention_noalloc``: the split partials go to the
+    library's static per-GPU scratch (no workspace; calls overlapping on one GPU race).  ``out`` must be given by
+    callers that cannot allocate."""
+    _req(q.dim() == 3, "q must be [batch, num_heads, head_dim]")
+    batch, num_heads, head_dim = q.shape
+    _, kvh, psize, hd = _check_pool(q, k_pool, v_pool, page_table, seq_lens, num_heads, False)
+    _req(hd == head_dim and page_table.shape[0] == batch and seq_lens.shape == (batch,), "shape mismatch")
+    out = torch.empty_like(q) if out is None else out
+    _cuda(out, "out")
+    _req(out.shape == q.shape and out.dtype == q.dtype, "out must match q")
+    scale = 1.0 / math.sqrt(head_dim) if scale is None else scale
+    hip.call("cir_paged_decode_attention_noalloc", q.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(),
+             page_table.data_ptr(), seq_lens.data_ptr(), out.data_ptr(), batch, num_heads, kvh, head_dim, psize,
+             page_table.shape[1], float(scale), hip.dtype_code(q.dtype), hip.stream_handle())
+    return out
+
+
 def paged_decode_attention_qkv(part, inv_freq, positions, k_pool, v_pool, page_table, seq_lens, *, num_heads: int,
                                scale: float | None = None, out: torch.Tensor | None = None,
                                workspace: torch.Tensor | None = None, check_tables: bool = False) -> torch.Tensor:

@@ -62,6 +62,25 @@ int cir_paged_decode_attention(const void* q, const void* k_pool, const void* v_
                                int batch, int num_heads, int num_kv_heads, int head_dim,
                                int page_size, int max_pages, float scale, int kv_dtype, void* stream);
 
+/* cir_paged_decode_attention without a workspace argument, for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  No counterpart in the reference.  It allocates nothing: the split
+ * partials go to a static device array of CIR_ATTENTION_NOALLOC_MAX_BYTES per GPU,
+ * looked up on the first call on each device (make the stream's device current).
+ * Sizes whose partials, rows * num_heads * S * (head_dim + 2) * 4 bytes with S the
+ * split count, exceed it return hipErrorInvalidValue before launching (the fp16
+ * head_dim-128 path never splits beyond 256 workgroups, so it fits at any batch; the
+ * generic path needs 4 * num_heads * (head_dim + 2) bytes per 128 tokens per row).
+ * Results are bitwise those of cir_paged_decode_attention.  Every call on one GPU
+ * shares the array: calls that overlap on one GPU (two streams, two host threads)
+ * race and must be serialised by the caller.  Nothing in the array needs clearing:
+ * each launch writes every partial it reads. */
+#define CIR_ATTENTION_NOALLOC_MAX_BYTES ((size_t)16 << 20)
+int cir_paged_decode_attention_noalloc(const void* q, const void* k_pool, const void* v_pool,
+                                       const int32_t* page_table, const int32_t* seq_lens, void* out,
+                                       int batch, int num_heads, int num_kv_heads, int head_dim,
+                                       int page_size, int max_pages, float scale, int kv_dtype, void* stream);
+
 /* Decode attention fused with the QKV epilogue: instead of a finished q it takes the
  * QKV projection's fp32 split-k partials [splits][batch][(num_heads + 2 num_kv_heads)
  * head_dim] (q | k | v columns, as cir_qgemm writes them), applies interleaved RoPE

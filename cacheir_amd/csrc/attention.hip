@@ -517,7 +517,9 @@ __global__ __launch_bounds__(64) void attn_chunk_generic(
 // Latency-bound (a few KiB per workgroup), so no load waits for another: thread s
 // reads split s's (m, l), the weights 2^(m_s - M) go through LDS, and each output
 // element's S partials are loaded 8 at a time before they are summed.  Sums run in
-// split order, as the serial form for S > kMergeFast does.
+// split order, as the serial form for S > kMergeFast does.  o * inv is rounded to fp32
+// before the fp16 conversion (as_f32_value: no single-rounding mixed-precision multiply),
+// the same two roundings the O projection's merge (qgemm.hip, attn_merged_chunk) makes.
 constexpr int kMergeFast = 128;
 template <typename T>
 __global__ __launch_bounds__(128) void attn_merge(const float* __restrict__ part_o, const float* __restrict__ part_ml,
@@ -551,7 +553,7 @@ __global__ __launch_bounds__(128) void attn_merge(const float* __restrict__ part
         for (int j = 0; j < 8; ++j)
           if (s0 + j < S) o = fmaf(v[j], sw[s0 + j], o);
       }
-      out[((size_t)row * Hq + head) * D + d] = from_f32<T>(o * inv);
+      out[((size_t)row * Hq + head) * D + d] = from_f32<T>(as_f32_value(o * inv));
     }
     return;
   }
@@ -566,7 +568,7 @@ __global__ __launch_bounds__(128) void attn_merge(const float* __restrict__ part
     float o = 0.f;
     if (M != -INFINITY)
       for (int s = 0; s < S; ++s) o = fmaf(po[(size_t)s * D + d], exp2f(ml[2 * s] - M), o);
-    out[((size_t)row * Hq + head) * D + d] = from_f32<T>(o * inv);
+    out[((size_t)row * Hq + head) * D + d] = from_f32<T>(as_f32_value(o * inv));
   }
 }
 

@@ -853,8 +853,10 @@ struct AttnParts {
 constexpr int kAttnMaxParts = 8;
 
 // 8 consecutive head dims (d0..d0+7) of one (row, head) of the merged attention output,
-// rounded to fp16 with the arithmetic and order of attn_merge (attention.hip).  About
-// one value in 16k still rounds one fp16 ulp away from the stored attention output.
+// rounded to fp16 with the arithmetic and order of attn_merge (attention.hip): the same
+// fmaf chains and o * inv rounded to fp32 before the fp16 conversion in both (left to
+// itself the compiler fuses one of them into a single-rounding v_fma_mixlo_f16, which
+// put one value in ~16k one fp16 ulp apart), so both paths give the same bits.
 // All loads are issued first.
 __device__ __forceinline__ u32x4 attn_merged_chunk(const AttnParts& a, int row, int head, int d0) {
   const float* ml = a.ml + ((size_t)row * a.heads + head) * a.S * 2;
@@ -892,7 +894,7 @@ __device__ __forceinline__ u32x4 attn_merged_chunk(const AttnParts& a, int row, 
   uint32_t h[4];
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
-    const f16x2 two = {static_cast<f16>(o[2 * e] * inv), static_cast<f16>(o[2 * e + 1] * inv)};
+    const f16x2 two = {static_cast<f16>(as_f32_value(o[2 * e] * inv)), static_cast<f16>(as_f32_value(o[2 * e + 1] * inv))};
     h[e] = __builtin_bit_cast(uint32_t, two);
   }
   return u32x4{h[0], h[1], h[2], h[3]};
@@ -1620,4 +1622,29 @@ extern "C" int cir_qgemm_argmax(const void* x, int ldx, const void* w_tiled, int
   else if (fmt == CIR_I4_ROW) go.template operator()<CIR_I4_ROW>();
   else go.template operator()<CIR_I8_ROW>();
   return launch_status();
+}
+
+extern "C" const char* cir_qgemm_plan(int op, int fmt, int m, int n, int k, int splits) {
+  if (!valid_fmt(fmt) || m <= 0 || n <= 0 || k <= 0 || k % 128) return "invalid";
+  switch (op) {
+    case CIR_GEMM_PARTIALS:
+      if (splits < 1 || (k / 128) % splits) return "invalid";
+      if (gemv_fits(m, k, splits)) return "qgemv_kernel";
+      if (m <= 16) return "qgemm_xs_kernel<NT=1,MT=1>";
+      if (!use_xl(m, n)) return "qgemm_xs_kernel<NT=2,MT=2>";
+      return m <= 64 ? "qgemm_xl_kernel<MT=4>" : "qgemm_xl_kernel<MT=8>";
+    case CIR_GEMM_SWIGLU:
+      if (use_xl(m, n)) return xl_mt(m) == 4 ? "qgemm_xl_kernel<MT=4,EPI=swiglu>" : "qgemm_xl_kernel<MT=8,EPI=swiglu>";
+      return m <= 16 ? "qgemm_xs_kernel<NT=2,MT=1,EPI=swiglu>" : "qgemm_xs_kernel<NT=2,MT=2,EPI=swiglu>";
+    case CIR_GEMM_ARGMAX:
+      if (gemv_head_fits(fmt, m, k)) return "qgemv_kernel<EPI=argmax>+argmax_cand_kernel";
+      return m <= 16 ? "qgemm_xs_kernel<NT=1,MT=1,EPI=argmax>+argmax_cand_kernel"
+                     : "qgemm_xs_kernel<NT=2,MT=2,EPI=argmax>+argmax_cand_kernel";
+    case CIR_GEMM_ATTN_MERGE:
+      if ((fmt != CIR_Q4_0 && fmt != CIR_Q8_0) || splits < 1 || (k / 128) % splits || !gemv_fits(m, k, splits))
+        return "invalid";
+      return "qgemv_kernel<input=attention partials>";
+    default:
+      return "invalid";
+  }
 }

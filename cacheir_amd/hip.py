@@ -25,6 +25,7 @@ CIR_Q8_0 = 8
 CIR_I4_ROW = 64  # the reference's per-row asymmetric int4 packing
 CIR_I8_ROW = 65  # ... and int8
 ATTENTION_NOALLOC_MAX_BYTES = 16 << 20  # CIR_ATTENTION_NOALLOC_MAX_BYTES
+GEMM_PARTIALS, GEMM_SWIGLU, GEMM_ARGMAX, GEMM_ATTN_MERGE = 0, 1, 2, 3  # cir_qgemm_plan ops
 
 _c_int, _c_size, _c_float, _vp = ctypes.c_int, ctypes.c_size_t, ctypes.c_float, ctypes.c_void_p
 
@@ -51,6 +52,7 @@ _SIGNATURES = {
     "cir_qgemm_splits": (_c_int, [_c_int, _c_int, _c_int]),
     "cir_qgemm_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int]),
     "cir_qgemm": (_c_int, [_vp, _c_int, _vp, _c_int, _vp, _c_int, _c_int, _c_int, _c_int, _vp]),
+    "cir_qgemm_plan": (ctypes.c_char_p, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int]),
     "cir_qgemm_attn": (_c_int, [_vp, _vp, _c_int, _c_int, _vp, _c_int, _vp, _c_int, _c_int, _c_int, _c_int, _vp]),
     "cir_qgemm_swiglu": (_c_int, [_vp, _c_int, _vp, _c_int, _vp, _c_int, _c_int, _c_int, _c_int, _vp]),
     "cir_qgemm_argmax_workspace_bytes": (_c_size, [_c_int, _c_int]),

@@ -39,7 +39,8 @@ def _cuda(t: torch.Tensor, name: str, rows_only: bool = False) -> None:
 # ------------------------------------------------------------------ attention --
 def attention_workspace(rows: int, num_heads: int, head_dim: int, max_context: int, device) -> torch.Tensor:
     n = hip.size_call("cir_paged_attention_workspace_bytes", rows, num_heads, head_dim, max_context)
-    return torch.zeros(max(n, 4), dtype=torch.uint8, device=device)  # ticket counters must start at zero
+    # holds split partials O and (max, sum), each written before it is read: no clearing needed
+    return torch.empty(max(n, 4), dtype=torch.uint8, device=device)
 
 
 def _check_pool(q, k_pool, v_pool, page_table, seq_lens, num_heads, check_tables):
@@ -263,6 +264,11 @@ def qgemm_attn(workspace: torch.Tensor, attn_splits: int, num_heads: int, w: QWe
     hip.call("cir_qgemm_attn", base, base + 4 * o_floats, attn_splits, num_heads, w.tiled.data_ptr(), w.fmt,
              out.data_ptr(), m, w.n, w.k, splits, hip.stream_handle())
     return out.view(-1)[: splits * m * w.n].view(splits, m, w.n)
+
+
+def gemm_plan(op: int, fmt: int, m: int, n: int, k: int, splits: int = 1) -> str:
+    """Name of the kernel the library runs for this GEMM (``cir_qgemm_plan``; op = ``hip.GEMM_*``)."""
+    return hip.load().cir_qgemm_plan(op, fmt, m, n, k, splits).decode()
 
 
 def choose_splits(m: int, n: int, k: int) -> int:

@@ -159,12 +159,26 @@ class StepPlan:
         self.generation = rt.kv_allocator.generation
         dev = rt.device
         self.rows = rows = batch * q_len
-        self.ids = torch.zeros(rows, dtype=torch.int64, device=dev)
-        self.positions = torch.zeros(batch, dtype=torch.int32, device=dev)
-        self.seq_lens = torch.zeros(batch, dtype=torch.int32, device=dev)
-        self.page_table = torch.zeros((batch, max_pages), dtype=torch.int32, device=dev)
+        # The step inputs live in one int32 device buffer (ids as int64 pairs, positions, seq_lens, page table)
+        # filled from one pinned host buffer by one copy per step; the launches below read these views, so a
+        # captured graph replays with whatever the last copy wrote.
+        self._in_pos = 2 * rows
+        self._in_len = self._in_pos + batch
+        self._in_pt = self._in_len + batch
+        total = self._in_pt + batch * max_pages
+        self._in_dev = torch.zeros(total, dtype=torch.int32, device=dev)
+        self._in_host = torch.zeros(total, dtype=torch.int32, pin_memory=True)
+        self._in_np = self._in_host.numpy()
+        self._in_copied = torch.cuda.Event()
+        self._in_pending = False
+        self.ids = self._in_dev[: 2 * rows].view(torch.int64)
+        self.positions = self._in_dev[self._in_pos: self._in_len]
+        self.seq_lens = self._in_dev[self._in_len: self._in_pt]
+        self.page_table = self._in_dev[self._in_pt:].view(batch, max_pages)
         self.launches: list = []
         self.graph_obj: torch.cuda.CUDAGraph | None = None
+        self.graphs: dict[str, torch.cuda.CUDAGraph] = {}  # "logits" / "greedy" -> captured step
+        self.replays = 0
         self._head: tuple | None = None  # (x, lm_head weight, workspace) when the greedy head can be fused
         self._head_at = 0
         self._gemm_need = 1
@@ -172,7 +186,9 @@ class StepPlan:
         self.gemm_ws = torch.empty(self._gemm_need, dtype=torch.float32, device=dev)
         attn_need = kernels.hip.size_call("cir_paged_attention_workspace_bytes", rows, rt.config.num_attention_heads,
                                           rt.config.head_dim, max_pages * rt.kv_allocator.page_size)
-        self.attn_ws = torch.zeros(max(attn_need, 4), dtype=torch.uint8, device=dev)  # zeroed once; calls leave it zeroed
+        # split partials of the attention (and of the O projection's merge at batch <= 8): every launch writes
+        # what it later reads, so the buffer needs no clearing
+        self.attn_ws = torch.empty(max(attn_need, 4), dtype=torch.uint8, device=dev)
 
     # ------------------------------------------------------------------ build --
     def _fuse_qkv_into_attention(self, users, k_pool: torch.Tensor, head_dim: int) -> bool:
@@ -225,6 +241,7 @@ class StepPlan:
                 self.launches.append(lambda w=weight, s=splits, S=S, h=heads: kernels.qgemm_attn(
                     self.attn_ws, S, h, w, rows, splits=s, out=self.gemm_ws))
                 rt._count("rocm.attn_merge_qgemv")
+                rt._record_gemm_plan(hip.GEMM_ATTN_MERGE, weight, rows, splits)
                 part = lambda s=splits, n=n: self.gemm_ws[: s * rows * n].view(s, rows, n)
                 return part, splits, n
             if isinstance(weight, kernels.QWeight):
@@ -235,6 +252,7 @@ class StepPlan:
                 self.launches.append(lambda x=x, w=weight, s=splits: kernels.qgemm_partial(x, w, splits=s,
                                                                                            out=self.gemm_ws))
                 rt._count("rocm.qgemm_blocks")
+                rt._record_gemm_plan(hip.GEMM_PARTIALS, weight, rows, splits)
             else:
                 n, k = weight.shape
                 splits = 1
@@ -298,10 +316,14 @@ class StepPlan:
                     _, part, inv, _ = qin
                     S = kernels.paged_decode_splits(self.batch, heads, kp.shape[1], hd, kp.shape[2], self.max_pages,
                                                     kp.dtype)
-                    self.launches.append(lambda part=part, inv=inv, kp=kp, vp=vp, h=heads:
-                                         kernels.paged_decode_attention_qkv_parts(
-                                             part(), inv, self.positions, kp, vp, self.page_table, self.seq_lens,
-                                             num_heads=h, workspace=self.attn_ws))
+                    def attn_parts(part=part, inv=inv, kp=kp, vp=vp, h=heads, S=S):
+                        got = kernels.paged_decode_attention_qkv_parts(
+                            part(), inv, self.positions, kp, vp, self.page_table, self.seq_lens, num_heads=h,
+                            workspace=self.attn_ws)
+                        if got != S:  # the O projection below reads the workspace laid out for S splits
+                            raise RuntimeError(f"decode attention used {got} context splits, the plan expects {S}")
+
+                    self.launches.append(attn_parts)
                     rt._count("rocm.rope_kv_append_paged_attention_decode_parts")
                     env[outs[0]] = ("attn-parts", S, heads)
                     continue
@@ -333,6 +355,7 @@ class StepPlan:
                     x16 = as_dtype(env[ins[0]], torch.float16)
                     self._head_at = len(self.launches)
                     self._head = (x16, W, kernels.qgemm_argmax_workspace(rows, W.n, rt.device))
+                    rt._record_gemm_plan(hip.GEMM_ARGMAX, W, rows, 1)
                     env[ins[0]] = x16
                 part, _, n = gemm(env[ins[0]], W)
                 users = consumers.get(outs[0], [])
@@ -392,6 +415,7 @@ class StepPlan:
                     out = buf(inter, odt)
                     self.launches.append(lambda x=x, w=W, o=out: kernels.qgemm_swiglu(x, w, o.dtype, out=o))
                     rt._count("rocm.qgemm_swiglu")
+                    rt._record_gemm_plan(hip.GEMM_SWIGLU, W, rows, 1)
                     env[outs[0]] = out
                     continue
                 W = rt.weights.matmul_weight((ins[1], ins[2]))
@@ -434,12 +458,19 @@ class StepPlan:
 
     # ------------------------------------------------------------------ run ----
     def set_inputs(self, ids: np.ndarray, page_rows: np.ndarray, positions: np.ndarray) -> None:
-        """Host -> device copies of the step inputs (into the static buffers)."""
-        self.ids.copy_(torch.from_numpy(np.ascontiguousarray(ids, dtype=np.int64).reshape(-1)))
-        self.page_table.copy_(torch.from_numpy(np.ascontiguousarray(page_rows, dtype=np.int32)))
-        pos = np.ascontiguousarray(positions, dtype=np.int32)
-        self.positions.copy_(torch.from_numpy(pos))
-        self.seq_lens.copy_(torch.from_numpy(pos + np.int32(self.q_len)))
+        """Stage the step inputs in the pinned buffer and copy them to the device buffer (one async copy, stream
+        ordered before the step).  Waits first for the previous copy to have left the pinned buffer."""
+        if self._in_pending:
+            self._in_copied.synchronize()
+        h, B, rows = self._in_np, self.batch, self.rows
+        h[: 2 * rows].view(np.int64)[:] = np.asarray(ids, dtype=np.int64).reshape(-1)
+        pos = np.asarray(positions, dtype=np.int32).reshape(-1)
+        h[self._in_pos: self._in_len] = pos
+        h[self._in_len: self._in_pt] = pos + np.int32(self.q_len)
+        h[self._in_pt:].reshape(B, self.max_pages)[:] = page_rows
+        self._in_dev.copy_(self._in_host, non_blocking=True)
+        self._in_copied.record()
+        self._in_pending = True
 
     def launch(self) -> None:
         for fn in self.launches:
@@ -480,18 +511,35 @@ class StepPlan:
             raise RuntimeError("plan has not been captured")
         self.graph_obj.replay()
 
+    def run_graph(self, kind: str) -> None:
+        """The step as a HIP graph replay: ``"logits"`` (the logits buffer) or ``"greedy"`` (next_ids through the
+        fused head).  Captured on first use: the capture's eager warm-up on a side stream computes this step
+        (capturing itself runs nothing); later calls replay the graph over the inputs ``set_inputs`` copied.
+        The static inputs are those of ``cacheir/backends/cuda_graphs.py:38-55``: ids, page table, lengths."""
+        g = self.graphs.get(kind)
+        if g is None:
+            self.graphs[kind] = self.capture(with_argmax=False, greedy=(kind == "greedy"))
+            self.rt._count("rocm.graph_capture")
+        else:
+            g.replay()
+            self.replays += 1
+
 
 # ========================================================================= runtime ==
 class HipRuntime:
-    """Execute compiled CacheIR graphs on an MI355X through the cacheir_amd HIP kernels."""
+    """Execute compiled CacheIR graphs on an MI355X through the cacheir_amd HIP kernels.
+
+    Decode steps (``run`` in decode mode, ``run_decode_batch``, ``decode_greedy``) replay a HIP graph of the
+    step captured once per (batch, page-table width, pool generation); only the inputs are copied per step
+    (``use_graphs=False`` launches the same kernels one by one instead).  Prefill launches eagerly."""
 
     supports_variable_prefill_batch = True
 
     def __init__(self, artifact: CompileArtifact | str | Path, *, device: str = "cuda", dtype: str | None = "auto",
                  weights: HipWeightStore | None = None, source=None, tokenizer=None,
                  prefix_cache: PrefixCache | None = None, kv_allocator: HipKVPageAllocator | None = None,
-                 kv_capacity_pages: int = 64, memory_limit_mb: float | None = None,
-                 _plans: dict | None = None, _inv_freq: dict | None = None):
+                 kv_capacity_pages: int = 64, memory_limit_mb: float | None = None, use_graphs: bool = True,
+                 _plans: dict | None = None, _inv_freq: dict | None = None, _gemm_plans: OrderedDict | None = None):
         if not torch.cuda.is_available():
             raise RuntimeError("HipRuntime requested a GPU, but torch.cuda.is_available() is false")
         hip.load()  # no CPU fallback: fail here if the kernel library is missing
@@ -519,11 +567,14 @@ class HipRuntime:
         if self.kv_allocator.dtype != self.dtype:
             raise ValueError("kv_allocator dtype differs from the runtime dtype")
         self.kv_cache = HipPagedKVCache(self.kv_allocator)
+        self._extra_rows: list[HipPagedKVCache] = []  # rows 1.. of a multi-row run([B, S]) batch
         self.prefix_cache = prefix_cache or PrefixCache(capacity=8)
         self.memory_limit_mb = memory_limit_mb
+        self.use_graphs = bool(use_graphs)
         self._plans: dict = _plans if _plans is not None else {}
         self._inv_freq: dict = _inv_freq if _inv_freq is not None else {}
         self.kernel_counts: OrderedDict[str, int] = OrderedDict()
+        self.gemm_plans: OrderedDict[str, str] = _gemm_plans if _gemm_plans is not None else OrderedDict()
         self.oom_recoveries = 0
 
     # ------------------------------------------------------------- helpers --
@@ -546,6 +597,14 @@ class HipRuntime:
 
     def _count(self, name: str) -> None:
         self.kernel_counts[name] = self.kernel_counts.get(name, 0) + 1
+
+    def _record_gemm_plan(self, op: int, w: "kernels.QWeight", m: int, splits: int) -> None:
+        """``gemm_plans`` entry for a projection, keyed as the reference keys them (``cuda.py:956-974``):
+        ``(m, k)x(n, k)`` -> the kernel the library runs and its k-split."""
+        n = w.n
+        kernel = kernels.gemm_plan(op, w.fmt, m, n, w.k, splits)
+        tag = {hip.GEMM_SWIGLU: "swiglu:", hip.GEMM_ARGMAX: "argmax:", hip.GEMM_ATTN_MERGE: "attn_merge:"}.get(op, "")
+        self.gemm_plans[f"{tag}{(m, w.k)}x{(n, w.k)}"] = f"rocm.{kernel} splits={splits}"
 
     def inv_freq(self, head_dim: int, theta: float) -> torch.Tensor:
         key = (head_dim, float(theta))
@@ -579,9 +638,31 @@ class HipRuntime:
 
     def _recover_from_oom(self) -> None:
         self.oom_recoveries += 1
-        self.kv_cache.clear()
+        self._clear_rows()
         self._plans.clear()
         torch.cuda.empty_cache()
+
+    def _clear_rows(self) -> None:
+        self.kv_cache.clear()
+        for c in self._extra_rows:
+            c.clear()
+        self._extra_rows = []
+
+    def _row_caches(self, rows: int) -> list[HipPagedKVCache]:
+        """The KV caches of a ``run`` over ``rows`` sequences: ``kv_cache`` holds row 0, further rows get caches of
+        their own on the shared pool.  The row count may change only while every row is empty."""
+        caches = [self.kv_cache] + self._extra_rows
+        if len(caches) != rows:
+            if any(c.tokens for c in caches):
+                raise ValueError(f"input has {rows} rows but the session's KV cache holds {len(caches)}; "
+                                 "prefill with reset_kv to change the batch")
+            for c in self._extra_rows:
+                c.clear()
+            self._extra_rows = [HipPagedKVCache(self.kv_allocator) for _ in range(rows - 1)]
+            caches = [self.kv_cache] + self._extra_rows
+        elif len({c.tokens for c in caches}) > 1:
+            raise ValueError("the rows of a run([B, S]) batch hold different lengths")
+        return caches
 
     # -------------------------------------------------------------- API -----
     @classmethod
@@ -592,24 +673,25 @@ class HipRuntime:
         """New session sharing artifact, weights, tokenizer, prefix cache, plans and the KV allocator."""
         return HipRuntime(self.artifact, device=str(self.device), dtype=self._dtype_name(), weights=self.weights,
                           tokenizer=self.tokenizer, prefix_cache=self.prefix_cache, kv_allocator=self.kv_allocator,
-                          memory_limit_mb=self.memory_limit_mb, _plans=self._plans, _inv_freq=self._inv_freq)
+                          memory_limit_mb=self.memory_limit_mb, use_graphs=self.use_graphs, _plans=self._plans,
+                          _inv_freq=self._inv_freq, _gemm_plans=self.gemm_plans)
 
     def _dtype_name(self) -> str:
         return "float16" if self.dtype == torch.float16 else "float32"
 
-    def _prepare(self, sessions: list["HipRuntime"], ids: np.ndarray, mode: str) -> "StepPlan":
+    def _prepare(self, caches: list[HipPagedKVCache], ids: np.ndarray, mode: str) -> "StepPlan":
         """Reserve and map the KV pages the step writes, and load the step inputs into its plan."""
         batch, q_len = ids.shape
         P = self.kv_allocator.page_size
-        need_pages = sum(max(0, -(-(s.kv_cache.tokens + q_len) // P) - len(s.kv_cache.slots)) for s in sessions)
+        need_pages = sum(max(0, -(-(c.tokens + q_len) // P) - len(c.slots)) for c in caches)
         self.kv_allocator.reserve(need_pages)  # grow (and re-base pools) before any plan is built
-        positions = np.array([s.kv_cache.tokens for s in sessions], dtype=np.int32)
-        for s in sessions:
-            s.kv_cache.ensure_capacity(s.kv_cache.tokens + q_len)
-        max_pages = self._bucket(max(len(s.kv_cache.slots) for s in sessions))
+        positions = np.fromiter((c.tokens for c in caches), dtype=np.int32, count=batch)
+        for c in caches:
+            c.ensure_capacity(c.tokens + q_len)
+        max_pages = self._bucket(max(len(c.slots) for c in caches))
         rows = np.zeros((batch, max_pages), dtype=np.int32)
-        for b, s in enumerate(sessions):
-            rows[b, : len(s.kv_cache.slots)] = s.kv_cache.slots
+        for b, c in enumerate(caches):
+            rows[b, : len(c.slots)] = c.slots
         self._enforce_memory_limit()
         try:
             plan = self.plan(mode, batch, q_len, max_pages)
@@ -620,33 +702,46 @@ class HipRuntime:
                                "retry with a smaller batch/context") from exc
         return plan
 
-    def _execute(self, sessions: list["HipRuntime"], ids: np.ndarray, mode: str) -> torch.Tensor:
-        batch, q_len = ids.shape
-        plan = self._prepare(sessions, ids, mode)
+    def _step(self, caches: list[HipPagedKVCache], ids: np.ndarray, mode: str, greedy: bool = False) -> StepPlan:
+        """One step over ``caches``: a graph replay for decode (when ``use_graphs``), eager launches otherwise.
+        ``greedy`` runs the fused LM head + argmax (``plan.next_ids``) instead of writing the logits."""
+        q_len = ids.shape[1]
+        plan = self._prepare(caches, ids, mode)
         try:
-            plan.launch()
+            if self.use_graphs and mode == "decode":
+                plan.run_graph("greedy" if greedy else "logits")
+            elif greedy:
+                plan.launch_greedy()
+            else:
+                plan.launch()
         except torch.cuda.OutOfMemoryError as exc:
             self._recover_from_oom()
             raise RuntimeError("CacheIR HIP runtime recovered from an out-of-memory condition; "
                                "retry with a smaller batch/context") from exc
-        for s in sessions:
-            s.kv_cache.tokens += q_len
+        for c in caches:
+            c.tokens += q_len
+        return plan
+
+    def _execute(self, caches: list[HipPagedKVCache], ids: np.ndarray, mode: str) -> torch.Tensor:
+        batch, q_len = ids.shape
+        plan = self._step(caches, ids, mode)
         return plan.logits.view(batch, q_len, -1).clone()
 
     def run(self, input_ids, *, mode: str = "prefill", reset_kv: bool | None = None) -> torch.Tensor:
+        """``cuda.py:508-539``: ``input_ids`` ``[S]`` or ``[B, S]`` -> logits ``[B, S, V]``.  A ``[B, S]`` batch is
+        B sequences of this session, each with its own pages (prefill them together, then decode ``[B, 1]``)."""
         if reset_kv is None:
             reset_kv = mode == "prefill"
-        if mode == "prefill" and reset_kv:
-            self.kv_cache.clear()
         ids = np.asarray(input_ids, dtype=np.int64)
         if ids.ndim == 1:
             ids = ids[None, :]
-        if ids.ndim != 2 or ids.shape[0] != 1 or ids.shape[1] < 1:
-            raise ValueError("HipRuntime.run takes one sequence [1, seq]; use run_decode_batch / run_prefill_batch "
-                             "for several sessions")
+        if ids.ndim != 2 or ids.shape[0] < 1 or ids.shape[1] < 1:
+            raise ValueError("HipRuntime.run takes token ids [seq] or [batch, seq]")
         if mode == "decode" and ids.shape[1] != 1:
             raise ValueError("decode mode takes exactly one token per step")
-        return self._execute([self], ids, mode)
+        if mode == "prefill" and reset_kv:
+            self._clear_rows()
+        return self._execute(self._row_caches(ids.shape[0]), ids, mode)
 
     def _check_sessions(self, sessions) -> None:
         if not sessions:
@@ -660,9 +755,11 @@ class HipRuntime:
                 raise ValueError("all HIP sessions must use the same device")
             if s.kv_allocator is not self.kv_allocator:
                 raise ValueError("all HIP sessions must share one KV allocator (create them with fork())")
+            if s._extra_rows:
+                raise ValueError("a session holding a multi-row run([B, S]) batch cannot join a session batch")
 
     def run_decode_batch(self, sessions: list["HipRuntime"], token_ids) -> torch.Tensor:
-        """One decode token for several sessions in one launch sequence -> logits ``[B, 1, V]``."""
+        """One decode token for several sessions in one step -> logits ``[B, 1, V]`` (``cuda.py:541-582``)."""
         if not sessions:
             raise ValueError("run_decode_batch requires at least one session")
         if len(sessions) != len(token_ids):
@@ -670,7 +767,7 @@ class HipRuntime:
         self._check_sessions(sessions)
         ids = np.array([[int(t)] for t in token_ids], dtype=np.int64)
         self._count("cacheir.rocm_decode_batch_graph")
-        return self._execute(list(sessions), ids, "decode")
+        return self._execute([s.kv_cache for s in sessions], ids, "decode")
 
     def run_prefill_batch(self, sessions: list["HipRuntime"], token_id_batches: list[list[int]]) -> torch.Tensor:
         """Prefill several sessions -> logits ``[B, max_len, V]`` (rows past a prompt's end are zero)."""
@@ -683,13 +780,14 @@ class HipRuntime:
             raise ValueError("run_prefill_batch requires non-empty token batches")
         self._check_sessions(sessions)
         for s in sessions:
-            s.kv_cache.clear()
+            s._clear_rows()
         self._count("cacheir.rocm_prefill_batch_graph")
         if len(set(lens)) == 1:
-            return self._execute(list(sessions), np.array(token_id_batches, dtype=np.int64), "prefill")
+            return self._execute([s.kv_cache for s in sessions], np.array(token_id_batches, dtype=np.int64),
+                                 "prefill")
         out = torch.zeros((len(sessions), max(lens), self.config.vocab_size), dtype=torch.float32, device=self.device)
         for b, (s, toks) in enumerate(zip(sessions, token_id_batches)):
-            out[b, : len(toks)] = s._execute([s], np.array([toks], dtype=np.int64), "prefill")[0]
+            out[b, : len(toks)] = s._execute([s.kv_cache], np.array([toks], dtype=np.int64), "prefill")[0]
         return out
 
     def prefill_tokens(self, token_ids, *, use_prefix_cache: bool = False, remember_prefix: bool = False):
@@ -701,6 +799,7 @@ class HipRuntime:
         if use_prefix_cache and ids:
             prefix, pages = self.prefix_cache.longest_prefix(ids)
             if pages is not None and 0 < len(prefix) < len(ids) and pages.allocator is self.kv_allocator:
+                self._clear_rows()
                 self.kv_cache.alias_prefix(pages.slots, len(prefix))
                 reused = tuple(prefix)
                 logits = self.run([ids[len(prefix):]], mode="prefill", reset_kv=False)
@@ -725,16 +824,11 @@ class HipRuntime:
     def decode_greedy(self, sessions: list["HipRuntime"], token_ids) -> list[int]:
         """One decode step for ``sessions`` (one token each) returning the greedy next ids instead of logits
         (``run_decode_batch`` + argmax of scheduler.py:535-543, with the LM head and argmax fused)."""
+        if len(sessions) != len(token_ids):
+            raise ValueError("sessions and token_ids must have the same length")
+        self._check_sessions(sessions)
         ids = np.asarray(token_ids, dtype=np.int64).reshape(len(sessions), 1)
-        plan = self._prepare(sessions, ids, "decode")
-        try:
-            plan.launch_greedy()
-        except torch.cuda.OutOfMemoryError as exc:
-            self._recover_from_oom()
-            raise RuntimeError("CacheIR HIP runtime recovered from an out-of-memory condition; "
-                               "retry with a smaller batch/context") from exc
-        for s in sessions:
-            s.kv_cache.tokens += 1
+        plan = self._step([s.kv_cache for s in sessions], ids, "decode", greedy=True)
         return [int(v) % self.config.vocab_size for v in plan.next_ids.cpu().tolist()]
 
     def generate_ids(self, prompt_ids, max_new_tokens: int = 16) -> list[int]:
@@ -766,6 +860,11 @@ class HipRuntime:
         stats = self.kv_cache.stats()
         stats["prefix_cache"] = self.prefix_cache.stats()
         stats["kernel_counts"] = dict(self.kernel_counts)
+        stats["gemm_plans"] = dict(self.gemm_plans)
+        stats["step_graphs"] = {
+            f"{mode}:b{batch}:q{q_len}:p{pages}": {"captured": sorted(plan.graphs), "replays": plan.replays,
+                                                  "launches": len(plan.launches)}
+            for (mode, batch, q_len, pages), plan in self._plans.items() if plan.graphs}
         stats["oom_recoveries"] = self.oom_recoveries
         stats["memory_limit_mb"] = self.memory_limit_mb
         stats["weight_bytes"] = self.weights.nbytes()

@@ -173,10 +173,22 @@ size_t cir_qgemm_workspace_bytes(int m, int n, int splits);
 int cir_qgemm(const void* x, int ldx, const void* w_tiled, int fmt, float* y_partial,
               int m, int n, int k, int splits, void* stream);
 
+/* Which kernel the GEMM entry points run for these sizes (a static string; "invalid"
+ * for arguments the entry point would reject): op CIR_GEMM_PARTIALS = cir_qgemm with
+ * `splits`, CIR_GEMM_SWIGLU = cir_qgemm_swiglu (n = 2 * inter), CIR_GEMM_ARGMAX =
+ * cir_qgemm_argmax, CIR_GEMM_ATTN_MERGE = cir_qgemm_attn.  Pure host arithmetic.
+ * Replaces the reference's per-shape GEMM plan record (cacheir/runtime/cuda.py:956-974
+ * _select_gemm_plan, surfaced as CudaRuntime.gemm_plans, cuda.py:484,683-690). */
+#define CIR_GEMM_PARTIALS 0
+#define CIR_GEMM_SWIGLU 1
+#define CIR_GEMM_ARGMAX 2
+#define CIR_GEMM_ATTN_MERGE 3
+const char* cir_qgemm_plan(int op, int fmt, int m, int n, int k, int splits);
+
 /* The O projection of a decode step fed straight from split attention partials
  * (cir_paged_decode_attention_qkv_parts): the workgroup merges each head's S <= 8
- * partials into the fp16 attention output (the arithmetic of the attention's own merge;
- * about one value in 16k rounds one fp16 ulp apart) while staging its activations,
+ * partials into the fp16 attention output (the arithmetic and rounding of the attention's
+ * own merge, so the same bits) while staging its activations,
  * then runs as cir_qgemm.  Block formats,
  * k = num_heads * 128, m <= 8 with m * (k/128/splits) <= 256.  Replaces the
  * attention output -> o_proj quantized matmul pair (cacheir/runtime/cuda.py:932-954). */

@@ -14,6 +14,16 @@
 
 Weights are given as a dict ``value name -> float32 array`` (GGUF Q4_0/Q8_0 weights
 already decoded to float32 as ``gguf.py`` does at load).
+
+``OracleRuntime(..., fp16_storage=True)`` rounds values to float16 where a float16
+backend stores them (every matmul input, i.e. the normalised activations, the
+attention output and the SwiGLU output; q, k and v after RoPE, k and v as they enter
+the cache) and computes everything else in float32 as above.  It is the reference for
+an fp16 backend at the step level: in a randomly initialised network the attention
+softmax amplifies those storage roundings to ~1e-3 of the logits' scale, which the
+fp32 path cannot tell from a kernel error.  It restates no other arithmetic; it is
+pinned by the fp32 path (``fp16_storage=False`` gives the same results bit for bit as
+before) plus the points it rounds.
 """
 from __future__ import annotations
 
@@ -54,9 +64,11 @@ def create_tiny_weights(*, seed: int, vocab_size: int, hidden_size: int, interme
 class OracleRuntime:
     """One session: a compiled-graph dict per mode, weights by HF key, and a contiguous KV cache."""
 
-    def __init__(self, graphs: dict[str, dict], weights_by_key: dict[str, np.ndarray], vocab_size: int):
+    def __init__(self, graphs: dict[str, dict], weights_by_key: dict[str, np.ndarray], vocab_size: int,
+                 fp16_storage: bool = False):
         self.graphs = graphs
         self.vocab_size = vocab_size
+        self.fp16_storage = fp16_storage
         self.keys: dict[int, np.ndarray] = {}
         self.values: dict[int, np.ndarray] = {}
         self.weights = {}
@@ -67,6 +79,7 @@ class OracleRuntime:
     def fork(self) -> "OracleRuntime":
         other = OracleRuntime.__new__(OracleRuntime)
         other.graphs, other.vocab_size, other.weights = self.graphs, self.vocab_size, self.weights
+        other.fp16_storage = self.fp16_storage
         other.keys, other.values = {}, {}
         return other
 
@@ -99,23 +112,28 @@ class OracleRuntime:
             self.values[layer] = np.concatenate([self.values[layer], v], axis=1)
         return self.keys[layer], self.values[layer]
 
+    def _st(self, x: np.ndarray) -> np.ndarray:
+        """A value as a float16 backend stores it (identity unless ``fp16_storage``)."""
+        return x.astype(np.float16).astype(np.float32) if self.fp16_storage else x
+
     def _execute(self, node: dict, env: dict, mode: str) -> list[np.ndarray]:
         op, ins, attrs = node["op"], node["inputs"], node["attrs"]
+        st = self._st
         if op == "token_embedding":
             return [env[ins[1]][env[ins[0]]]]
         if op == "rms_norm":
             return [ops.rms_norm(env[ins[0]], env[ins[1]], float(attrs.get("eps", 1e-6)))]
         if op in {"matmul", "quantized_matmul"}:
-            return [ops.matmul(env[ins[0]], env[ins[1]])]
+            return [ops.matmul(st(env[ins[0]]), env[ins[1]])]
         if op == "qkv_projection":
-            x = env[ins[0]]
+            x = st(env[ins[0]])
             return [ops.matmul(x, env[ins[1]]), ops.matmul(x, env[ins[2]]), ops.matmul(x, env[ins[3]])]
         if op in {"fused_rmsnorm_qkv_rope", "quantized_fused_rmsnorm_qkv_rope"}:
-            x = ops.rms_norm(env[ins[0]], env[ins[1]], float(attrs.get("eps", 1e-6)))
+            x = st(ops.rms_norm(env[ins[0]], env[ins[1]], float(attrs.get("eps", 1e-6))))
             q, k, v = ops.matmul(x, env[ins[2]]), ops.matmul(x, env[ins[3]]), ops.matmul(x, env[ins[4]])
             off = self.kv_length(int(attrs.get("layer", 0)))
             hd, theta = int(attrs["head_dim"]), float(attrs.get("rope_theta", 10000.0))
-            return [ops.rope_one(q, hd, theta, off), ops.rope_one(k, hd, theta, off), v]
+            return [st(ops.rope_one(q, hd, theta, off)), st(ops.rope_one(k, hd, theta, off)), st(v)]
         if op == "rope":
             off = self.kv_length(int(attrs.get("layer", 0)))
             hd, theta = int(attrs["head_dim"]), float(attrs.get("rope_theta", 10000.0))
@@ -134,7 +152,7 @@ class OracleRuntime:
         if op == "elementwise_mul":
             return [env[ins[0]] * env[ins[1]]]
         if op in {"fused_swiglu", "quantized_fused_swiglu"}:
-            x = env[ins[0]]
+            x = st(env[ins[0]])
             return [ops.silu_mul(ops.matmul(x, env[ins[1]]), ops.matmul(x, env[ins[2]]))]
         raise NotImplementedError(f"oracle runtime does not implement op {op}")
 

@@ -334,3 +334,93 @@ def test_greedy_step_fuses_head_and_argmax(tmp_path, device):
         ref.append(nxt)
         lg = ref_rt.run([[nxt]], mode="decode")
     assert got == ref
+
+
+def test_decode_steps_replay_a_graph_equal_to_eager_launches(tmp_path, device):
+    """run_decode_batch and decode_greedy replay one captured HIP graph per (batch, page-table width): 8
+    consecutive steps over sessions whose positions cross page boundaries (and the page-table bucket 4 -> 8)
+    give logits and ids bitwise equal to the same steps launched kernel by kernel."""
+    from cacheir_amd.runtime import HipRuntime
+
+    cfg, w, blocks, decoded = _q4_model(tmp_path, "q4_0")
+    art = compile_config(cfg, quant="q4_0", model_path=str(write_model(tmp_path / "m", cfg, w)))
+    prompts = [list(range(3, 15)), list(range(20, 82)), [9] * 5]  # 12, 62, 5 tokens: pages 16, 64 are crossed
+    runs = {}
+    for use_graphs in (False, True):
+        base = HipRuntime(art, use_graphs=use_graphs)
+        sessions = [base.fork() for _ in prompts]
+        toks = [int(torch.argmax(s.run([p], mode="prefill")[0, -1])) for s, p in zip(sessions, prompts)]
+        logits, greedy = [], []
+        for step in range(8):
+            lg = base.run_decode_batch(sessions, toks)
+            logits.append(lg.cpu())
+            toks = [int(v) for v in lg[:, 0].argmax(dim=1).cpu()]
+            if step % 3 == 2:  # a greedy step in between: ids only
+                toks = base.decode_greedy(sessions, toks)
+                greedy.append(list(toks))
+        runs[use_graphs] = (logits, greedy, base.cache_stats())
+    (le, ge, se), (lg_, gg, sg) = runs[False], runs[True]
+    for a, b in zip(le, lg_):
+        assert torch.equal(a, b)
+    assert ge == gg
+    assert "rocm.graph_capture" not in se["kernel_counts"] and not se["step_graphs"]
+    assert sg["kernel_counts"]["rocm.graph_capture"] >= 3  # logits + greedy at page width 4, logits at 8
+    assert sum(e["replays"] for e in sg["step_graphs"].values()) >= 5
+
+
+def test_run_takes_a_batch_of_rows(tmp_path, device):
+    """run([B, S]) (cuda.py:508-539): B sequences of one session, each on pages of its own; prefill then decode
+    [B, 1] against the oracle, which runs the same [B, S] batch (cpu.py:111-140)."""
+    from cacheir_amd.runtime import HipRuntime
+
+    cfg, w, blocks, decoded = _q4_model(tmp_path, "q8_0")
+    art = compile_config(cfg, quant="q8_0", model_path=str(write_model(tmp_path / "m", cfg, w)))
+    rt = HipRuntime(art)
+    orc = OracleRuntime({m: g.to_dict() for m, g in art.graphs.items()}, decoded, cfg.vocab_size)
+    ids = [list(range(5, 23)), list(range(40, 58)), [7] * 18]
+    got = rt.run(ids, mode="prefill").cpu().numpy()
+    assert got.shape == (3, 18, cfg.vocab_size)
+    close16(got, orc.run(ids, mode="prefill"))
+    for _ in range(3):
+        nxt = [[int(np.argmax(r[-1]))] for r in got]
+        got = rt.run(nxt, mode="decode").cpu().numpy()
+        close16(got, orc.run(nxt, mode="decode"))
+    assert rt.kv_cache.tokens == 21 and all(c.tokens == 21 for c in rt._extra_rows)
+    with pytest.raises(ValueError):
+        rt.run([[1], [2]], mode="decode")  # the session holds 3 rows
+    # a new prefill with reset_kv may change the row count
+    one = rt.run([list(range(5, 23))], mode="prefill").cpu().numpy()
+    np.testing.assert_array_equal(one[0], rt.fork().run([list(range(5, 23))], mode="prefill").cpu().numpy()[0])
+
+
+@pytest.mark.parametrize("batch", [1, 4])
+def test_long_context_decode_merges_attention_in_the_o_projection(tmp_path, device, batch):
+    """At batch <= 8 with contexts past 256 tokens the decode attention splits its context and the O projection
+    merges the split partials while staging its input (cir_paged_decode_attention_qkv_parts + cir_qgemm_attn):
+    logits of that path against the oracle, over 300+ token prompts."""
+    from cacheir_amd.runtime import HipRuntime
+
+    cfg, w, blocks, decoded = _q4_model(tmp_path, "q4_0")
+    art = compile_config(cfg, quant="q4_0", model_path=str(write_model(tmp_path / "m", cfg, w)))
+    base = HipRuntime(art, kv_capacity_pages=256)
+    rng = np.random.default_rng(batch)
+    prompts = [rng.integers(0, cfg.vocab_size, 300 + 37 * b).tolist() for b in range(batch)]
+    sessions = [base.fork() for _ in range(batch)]
+    oracles = []
+    toks = []
+    for s, p in zip(sessions, prompts):
+        lg = s.run([p], mode="prefill")
+        o = OracleRuntime({m: g.to_dict() for m, g in art.graphs.items()}, decoded, cfg.vocab_size)
+        close16(lg.cpu().numpy()[:, -1], o.run([p], mode="prefill")[:, -1])
+        oracles.append(o)
+        toks.append(int(torch.argmax(lg[0, -1])))
+    for _ in range(3):
+        got = base.run_decode_batch(sessions, toks).cpu().numpy()
+        ref = np.concatenate([o.run([[t]], mode="decode") for o, t in zip(oracles, toks)], axis=0)
+        close16(got, ref)
+        toks = [int(np.argmax(r[-1])) for r in got]
+    counts = base.cache_stats()["kernel_counts"]
+    assert counts.get("rocm.attn_merge_qgemv", 0) > 0
+    assert counts.get("rocm.rope_kv_append_paged_attention_decode_parts", 0) > 0
+    plans = base.cache_stats()["gemm_plans"]
+    assert any(k.startswith("attn_merge:") for k in plans), plans

@@ -85,6 +85,9 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--gemm-iters", type=int, default=64)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first copy 256 MiB four times (the known-size kernel for FETCH_SIZE/WRITE_SIZE scaling)")
+    ap.add_argument("--only", choices=["gemm"], default=None,
+                    help="run only the projection rooflines (for rocprofv3 counter runs of the GEMM kernels) and "
+                         "print their JSON; not a bench line")
     return ap.parse_args()
 
 
@@ -161,6 +164,32 @@ def time_greedy_steps(plan, steps: int, warmup: int) -> float:
     return start.elapsed_time(end) / steps
 
 
+def time_runtime_steps(base, sessions, ids: list[int], steps: int, warmup: int) -> dict:
+    """Wall time per step of the runtime API with its host work: ``decode_greedy`` (inputs staged and copied,
+    the step's graph replayed, the ids copied back: a scheduler's greedy loop) and ``run_decode_batch`` followed by
+    a synchronize (logits left on the device).  Each step is rolled back one token afterwards, so every step decodes
+    at the same position over the same pages, as the graph-step timing does."""
+    import torch
+
+    def rollback():
+        for s in sessions:
+            s.kv_cache.tokens -= 1
+
+    out = {}
+    for name, fn in (("decode_greedy_ms", lambda: base.decode_greedy(sessions, ids)),
+                     ("run_decode_batch_ms", lambda: (base.run_decode_batch(sessions, ids), torch.cuda.synchronize()))):
+        for _ in range(max(2, warmup)):  # the first call captures the step's graph
+            fn()
+            rollback()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            fn()
+            rollback()
+        out[name] = round((time.perf_counter() - t0) * 1000.0 / steps, 4)
+    return out
+
+
 def ragged_attention_case(config: int, dev, iters: int) -> dict:
     """Paged decode attention at BASELINE config 2 (batch 64, Llama-3-8B heads, contexts
     U[512, 4096], pages permuted at random over the pool) or config 5 (batch 128, Qwen2-7B
@@ -229,94 +258,12 @@ def ragged_attention_case(config: int, dev, iters: int) -> dict:
     return res
 
 
-def main() -> int:
-    args = parse()
-    if args.gpus != 1:
-        print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); this build has no multi-GPU path",
-              flush=True)
-        return 2
+def gemm_rooflines(base, cfg, B, dev, args) -> dict:
+    """The projection rooflines: the fused gate|up GEMM + SwiGLU at m = batch, BASELINE config 3 (m = 1, 8, 32)
+    and the batched GEMM of config 5 (Q8_0 gate|up at m = 128), each timed live as HIP-graph replays."""
     import torch
 
-    from cacheir_amd.compiler import compile_config
-    from cacheir_amd.runtime import HipRuntime
-    from cacheir_amd.weights import GGML_Q4_0, SyntheticQuant
-
-    dev = torch.device("cuda:0")
-    if args.copy_calibration:
-        src = torch.ones(64 * 1024 * 1024, dtype=torch.float32, device=dev)
-        dst = torch.empty_like(src)
-        for _ in range(4):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        log(f"calibration: copied {src.numel() * 4} bytes x4")
-        del src, dst
-    cfg = llama3_8b(args.layers)
-    B, ctx, P = args.batch, args.ctx, 16
-    art = compile_config(cfg, quant="q4_0", modes=("decode",))
-    pages_per_seq = -(-ctx // P)
-    t0 = time.time()
-    base = HipRuntime(art, source=SyntheticQuant(GGML_Q4_0, dev, seed=0),
-                      kv_capacity_pages=B * pages_per_seq + 8)
-    sessions = [base.fork() for _ in range(B)]
-    for s in sessions:
-        s.kv_cache.ensure_capacity(ctx)
-        s.kv_cache.tokens = ctx - 1
-    g = torch.Generator(device=dev)
-    g.manual_seed(1)
-    for layer in range(cfg.num_layers):  # synthetic context: N(0,1) fp16 K/V in every page
-        base.kv_allocator.k[layer].normal_(generator=g)
-        base.kv_allocator.v[layer].normal_(generator=g)
-    max_pages = base._bucket(pages_per_seq)
-    plan = base.plan("decode", B, 1, max_pages)
-    rows = np.zeros((B, max_pages), np.int32)
-    for b, s in enumerate(sessions):
-        rows[b, : len(s.kv_cache.slots)] = s.kv_cache.slots
-    ids = np.random.default_rng(0).integers(0, cfg.vocab_size, size=(B, 1))
-    plan.set_inputs(ids, rows, np.full(B, ctx - 1, np.int32))
-    torch.cuda.synchronize()
-    log(f"model ready in {time.time() - t0:.1f}s; weights {base.weights.nbytes() / 1e9:.3f} GB, "
-        f"KV pool {base.kv_allocator.stats()['persistent_pools'][0]['bytes'] / 1e9:.3f} GB")
-
-    # the timed step is the greedy one (LM head fused with the argmax); check once that it picks the ids the
-    # logits path picks, and that the logits are finite
-    plan.launch_with_argmax()
-    torch.cuda.synchronize()
-    assert torch.isfinite(plan.logits).all().item(), "non-finite logits"
-    want = plan.next_ids.clone()
-    plan.next_ids.zero_()
-    plan.launch_greedy()
-    torch.cuda.synchronize()
-    assert torch.equal(plan.next_ids, want), "fused greedy head disagrees with argmax(logits)"
-
-    # Bytes a step must move: every linear weight and norm once, the embedding rows of
-    # the batch only (the table itself is never streamed), and every layer's K/V.  Taken
-    # before the roofline loops below tile extra weight copies into the same store.
-    embed = base.weights.dense("tok_embeddings", torch.float16)
-    weight_bytes = base.weights.nbytes() - embed.numel() * embed.element_size() + B * cfg.hidden_size * 2
-
-    ms_step = time_greedy_steps(plan, args.steps, args.warmup)
-    toks = B * 1000.0 / ms_step
-    assert bool(((plan.next_ids >= 0) & (plan.next_ids < cfg.vocab_size)).all().item()), "ids out of range"
-    log(f"step {ms_step:.3f} ms -> {toks:.1f} tok/s")
-
-    # ---- live roofline of the paged-attention kernel (HIP events on the launch stream) ----
     from cacheir_amd import kernels
-
-    H, Hkv, D = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
-    q = torch.randn((B, H, D), device=dev, dtype=torch.float16)
-    out = torch.empty_like(q)
-    ws = kernels.attention_workspace(B, H, D, max_pages * P, dev)
-    def attn(it):
-        kp, vp = base.kv_allocator.layer_pools(it % cfg.num_layers)
-        kernels.paged_decode_attention(q, kp, vp, plan.page_table, plan.seq_lens, out=out, workspace=ws)
-
-    attn_us = graph_us_per_launch(attn, args.attn_iters)
-    kv_bytes = 2 * Hkv * D * 2 * B * ctx  # K + V fp16 over every visible token
-    qo_bytes = 2 * B * H * D * 2
-    table_bytes = 4 * B * pages_per_seq + 4 * B
-    attn_bytes = kv_bytes + qo_bytes + table_bytes
-    achieved = attn_bytes / (attn_us * 1e-6) / 1e9
-    log(f"attention {attn_us:.2f} us/launch, {achieved:.0f} GB/s ({achieved / HBM_PEAK_GBS:.1%} of peak)")
 
     # ---- the same for the fused gate|up GEMM + SwiGLU (m = batch), rotated over the layers' weights ----
     gu = [base.weights.swiglu_weight(f"layer{i}_gate_w", f"layer{i}_up_w") for i in range(cfg.num_layers)]
@@ -372,6 +319,107 @@ def main() -> int:
     log(f"batched GEMM (config 5 gate|up Q8_0, m={m5}) {us5:.2f} us/launch, {tflops5:.0f} TFLOP/s "
         f"({tflops5 / MFMA_F16_PEAK_TFLOPS:.1%} of fp16 MFMA), {gbs5:.0f} GB/s")
     del w5
+    return {"us": gemm_us, "bytes": gemm_bytes, "gbs": gemm_gbs, "gemv": gemv, "us5": us5, "tflops5": tflops5,
+            "gbs5": gbs5}
+
+
+def main() -> int:
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); this build has no multi-GPU path",
+              flush=True)
+        return 2
+    import torch
+
+    from cacheir_amd.compiler import compile_config
+    from cacheir_amd.runtime import HipRuntime
+    from cacheir_amd.weights import GGML_Q4_0, SyntheticQuant
+
+    dev = torch.device("cuda:0")
+    if args.copy_calibration:
+        src = torch.ones(64 * 1024 * 1024, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(4):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"calibration: copied {src.numel() * 4} bytes x4")
+        del src, dst
+    cfg = llama3_8b(args.layers)
+    B, ctx, P = args.batch, args.ctx, 16
+    art = compile_config(cfg, quant="q4_0", modes=("decode",))
+    pages_per_seq = -(-ctx // P)
+    t0 = time.time()
+    base = HipRuntime(art, source=SyntheticQuant(GGML_Q4_0, dev, seed=0),
+                      kv_capacity_pages=B * pages_per_seq + 8)
+    sessions = [base.fork() for _ in range(B)]
+    for s in sessions:
+        s.kv_cache.ensure_capacity(ctx)
+        s.kv_cache.tokens = ctx - 1
+    g = torch.Generator(device=dev)
+    g.manual_seed(1)
+    for layer in range(cfg.num_layers):  # synthetic context: N(0,1) fp16 K/V in every page
+        base.kv_allocator.k[layer].normal_(generator=g)
+        base.kv_allocator.v[layer].normal_(generator=g)
+    max_pages = base._bucket(pages_per_seq)
+    plan = base.plan("decode", B, 1, max_pages)
+    rows = np.zeros((B, max_pages), np.int32)
+    for b, s in enumerate(sessions):
+        rows[b, : len(s.kv_cache.slots)] = s.kv_cache.slots
+    ids = np.random.default_rng(0).integers(0, cfg.vocab_size, size=(B, 1))
+    plan.set_inputs(ids, rows, np.full(B, ctx - 1, np.int32))
+    torch.cuda.synchronize()
+    log(f"model ready in {time.time() - t0:.1f}s; weights {base.weights.nbytes() / 1e9:.3f} GB, "
+        f"KV pool {base.kv_allocator.stats()['persistent_pools'][0]['bytes'] / 1e9:.3f} GB")
+
+    if args.only == "gemm":
+        gemm = gemm_rooflines(base, cfg, B, dev, args)
+        print(json.dumps({"only": "gemm", **gemm}), flush=True)
+        return 0
+
+    # the timed step is the greedy one (LM head fused with the argmax); check once that it picks the ids the
+    # logits path picks, and that the logits are finite
+    plan.launch_with_argmax()
+    torch.cuda.synchronize()
+    assert torch.isfinite(plan.logits).all().item(), "non-finite logits"
+    want = plan.next_ids.clone()
+    plan.next_ids.zero_()
+    plan.launch_greedy()
+    torch.cuda.synchronize()
+    assert torch.equal(plan.next_ids, want), "fused greedy head disagrees with argmax(logits)"
+
+    # Bytes a step must move: every linear weight and norm once, the embedding rows of
+    # the batch only (the table itself is never streamed), and every layer's K/V.  Taken
+    # before the roofline loops below tile extra weight copies into the same store.
+    embed = base.weights.dense("tok_embeddings", torch.float16)
+    weight_bytes = base.weights.nbytes() - embed.numel() * embed.element_size() + B * cfg.hidden_size * 2
+
+    ms_step = time_greedy_steps(plan, args.steps, args.warmup)
+    toks = B * 1000.0 / ms_step
+    assert bool(((plan.next_ids >= 0) & (plan.next_ids < cfg.vocab_size)).all().item()), "ids out of range"
+    log(f"step {ms_step:.3f} ms -> {toks:.1f} tok/s")
+
+    # ---- live roofline of the paged-attention kernel (HIP events on the launch stream) ----
+    from cacheir_amd import kernels
+
+    H, Hkv, D = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+    q = torch.randn((B, H, D), device=dev, dtype=torch.float16)
+    out = torch.empty_like(q)
+    ws = kernels.attention_workspace(B, H, D, max_pages * P, dev)
+    def attn(it):
+        kp, vp = base.kv_allocator.layer_pools(it % cfg.num_layers)
+        kernels.paged_decode_attention(q, kp, vp, plan.page_table, plan.seq_lens, out=out, workspace=ws)
+
+    attn_us = graph_us_per_launch(attn, args.attn_iters)
+    kv_bytes = 2 * Hkv * D * 2 * B * ctx  # K + V fp16 over every visible token
+    qo_bytes = 2 * B * H * D * 2
+    table_bytes = 4 * B * pages_per_seq + 4 * B
+    attn_bytes = kv_bytes + qo_bytes + table_bytes
+    achieved = attn_bytes / (attn_us * 1e-6) / 1e9
+    log(f"attention {attn_us:.2f} us/launch, {achieved:.0f} GB/s ({achieved / HBM_PEAK_GBS:.1%} of peak)")
+
+    gemm = gemm_rooflines(base, cfg, B, dev, args)
+    gemm_us, gemm_bytes, gemm_gbs = gemm['us'], gemm['bytes'], gemm['gbs']
+    gemv, us5, tflops5, gbs5 = gemm['gemv'], gemm['us5'], gemm['tflops5'], gemm['gbs5']
 
     # ---- the attention kernel at BASELINE configs 2 and 5 (ragged contexts, permuted / shared pages) ----
     ragged = []
@@ -388,6 +436,17 @@ def main() -> int:
     ms_b1 = time_greedy_steps(plan1, args.steps, args.warmup)
     kv_b1 = 2 * Hkv * D * 2 * ctx * cfg.num_layers
     log(f"batch-1 step {ms_b1:.3f} ms -> {1000.0 / ms_b1:.1f} tok/s")
+
+    # ---- the runtime API a scheduler calls, host work included (graph replay per step) ----
+    host_steps = {}
+    for name, sess, graph_ms in (("batch32", sessions, ms_step), ("batch1", sessions[:1], ms_b1)):
+        r = time_runtime_steps(base, sess, ids[: len(sess), 0].tolist(), args.steps, args.warmup)
+        r["graph_step_ms"] = round(graph_ms, 4)
+        r["decode_greedy_overhead"] = round(r["decode_greedy_ms"] / graph_ms - 1.0, 4)
+        host_steps[name] = r
+        log(f"runtime API {name}: decode_greedy {r['decode_greedy_ms']:.3f} ms, run_decode_batch "
+            f"{r['run_decode_batch_ms']:.3f} ms (graph step {graph_ms:.3f} ms)")
+    gemm_plans = base.cache_stats()["gemm_plans"]
 
     traffic = measured_traffic(TRAFFIC_FILE)
 
@@ -442,6 +501,10 @@ def main() -> int:
         "decode_batch1": {"ms_per_step": round(ms_b1, 4), "tokens_per_s": round(1000.0 / ms_b1, 2),
                           "hbm_floor_ms": round((weight_bytes + kv_b1) / HBM_PEAK_GBS / 1e6, 4),
                           "note": "same model and context, one sequence; projections on the dequant GEMV"},
+        "runtime_api_steps": {"note": "wall ms per step through HipRuntime.decode_greedy / run_decode_batch (+ "
+                                      "synchronize), host work included, graph replay per step",
+                              **host_steps},
+        "gemm_plans": gemm_plans,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

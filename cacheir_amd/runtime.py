@@ -467,7 +467,13 @@ class StepPlan:
         pos = np.asarray(positions, dtype=np.int32).reshape(-1)
         h[self._in_pos: self._in_len] = pos
         h[self._in_len: self._in_pt] = pos + np.int32(self.q_len)
-        h[self._in_pt:].reshape(B, self.max_pages)[:] = page_rows
+        table = h[self._in_pt:].reshape(B, self.max_pages)
+        if isinstance(page_rows, np.ndarray) and page_rows.ndim == 2:
+            table[:] = page_rows
+        else:  # one int32 row of slots per sequence, zero-padded to the plan's width
+            table[:] = 0
+            for b, r in enumerate(page_rows):
+                table[b, : len(r)] = r
         self._in_dev.copy_(self._in_host, non_blocking=True)
         self._in_copied.record()
         self._in_pending = True
@@ -689,9 +695,7 @@ class HipRuntime:
         for c in caches:
             c.ensure_capacity(c.tokens + q_len)
         max_pages = self._bucket(max(len(c.slots) for c in caches))
-        rows = np.zeros((batch, max_pages), dtype=np.int32)
-        for b, c in enumerate(caches):
-            rows[b, : len(c.slots)] = c.slots
+        rows = [c.slot_array() for c in caches]
         self._enforce_memory_limit()
         try:
             plan = self.plan(mode, batch, q_len, max_pages)

@@ -34,33 +34,47 @@ void orc_rmsnorm(const float* x, const float* w, float* out, int rows, int hidde
   }
 }
 
+/* 16 fp16 values -> fp32 (F16C / AVX-512 conversions). */
+static inline void h2f16(const uint16_t* src, float* dst) {
+#ifdef __AVX512F__
+  _mm512_storeu_ps(dst, _mm512_cvtph_ps(_mm256_loadu_si256((const __m256i*)src)));
+#else
+  _mm256_storeu_ps(dst, _mm256_cvtph_ps(_mm_loadu_si128((const __m128i*)src)));
+  _mm256_storeu_ps(dst + 8, _mm256_cvtph_ps(_mm_loadu_si128((const __m128i*)(src + 8))));
+#endif
+}
+
 /* y[m][n] (+)= sum_k x[m][k] * W[n][k] with W in GGUF Q4_0 blocks (18 bytes / 32 values);
- * accumulate != 0 adds into y (the residual add of cpu.py:256-257). M <= 64. */
+ * accumulate != 0 adds into y (the residual add of cpu.py:256-257). M <= 64.
+ * Each row keeps 16 lane sums (lane j adds columns 32b + j and 32b + 16 + j of every
+ * block b, in block order) reduced once at the end, so the inner loop is a plain
+ * 16-wide vector FMA without reassociating any sum. */
 void orc_q4_0_gemm(const float* x, int M, int K, const uint8_t* blocks, int N, float* y, int accumulate) {
   const int nb = K / 32;
 #pragma omp parallel for schedule(static)
   for (int n = 0; n < N; ++n) {
-    float acc[64];
-    for (int m = 0; m < M; ++m) acc[m] = 0.f;
+    float acc[64][16];
+    for (int m = 0; m < M; ++m)
+      for (int j = 0; j < 16; ++j) acc[m][j] = 0.f;
     const uint8_t* row = blocks + (size_t)n * nb * 18;
     for (int b = 0; b < nb; ++b) {
       const uint8_t* blk = row + (size_t)b * 18;
       const float d = h2f((uint16_t)(blk[0] | (blk[1] << 8)));
-      float w[32];
+      float lo[16], hi[16];
       for (int j = 0; j < 16; ++j) {
-        w[j] = (float)((int)(blk[2 + j] & 15) - 8) * d;
-        w[j + 16] = (float)((int)(blk[2 + j] >> 4) - 8) * d;
+        lo[j] = (float)((int)(blk[2 + j] & 15) - 8) * d;
+        hi[j] = (float)((int)(blk[2 + j] >> 4) - 8) * d;
       }
       for (int m = 0; m < M; ++m) {
         const float* xm = x + (size_t)m * K + (size_t)b * 32;
-        float s = 0.f;
-        for (int j = 0; j < 32; ++j) s += w[j] * xm[j];
-        acc[m] += s;
+        for (int j = 0; j < 16; ++j) acc[m][j] += lo[j] * xm[j] + hi[j] * xm[j + 16];
       }
     }
     for (int m = 0; m < M; ++m) {
-      if (accumulate) y[(size_t)m * N + n] += acc[m];
-      else y[(size_t)m * N + n] = acc[m];
+      float s = 0.f;
+      for (int j = 0; j < 16; ++j) s += acc[m][j];
+      if (accumulate) y[(size_t)m * N + n] += s;
+      else y[(size_t)m * N + n] = s;
     }
   }
 }
@@ -112,8 +126,15 @@ void orc_paged_attention(const float* q, const uint16_t* kp, const uint16_t* vp,
         float mx = -INFINITY;
         for (int t = 0; t < L; ++t) {
           const uint16_t* kr = kp + (((size_t)page_table[(size_t)b * max_pages + t / P] * Hkv + g) * P + t % P) * D;
+          float part[16] = {0.f}, kf[16];
+          int d = 0;
+          for (; d + 16 <= D; d += 16) {
+            h2f16(kr + d, kf);
+            for (int j = 0; j < 16; ++j) part[j] += qh[d + j] * kf[j];
+          }
           float s = 0.f;
-          for (int d = 0; d < D; ++d) s += qh[d] * h2f(kr[d]);
+          for (int j = 0; j < 16; ++j) s += part[j];
+          for (; d < D; ++d) s += qh[d] * h2f(kr[d]);
           sc[t] = s * scale;
           if (sc[t] > mx) mx = sc[t];
         }
@@ -127,7 +148,13 @@ void orc_paged_attention(const float* q, const uint16_t* kp, const uint16_t* vp,
         for (int t = 0; t < L; ++t) {
           const uint16_t* vr = vp + (((size_t)page_table[(size_t)b * max_pages + t / P] * Hkv + g) * P + t % P) * D;
           const float p = sc[t] / sum;
-          for (int d = 0; d < D; ++d) o[d] += p * h2f(vr[d]);
+          float vf[16];
+          int d = 0;
+          for (; d + 16 <= D; d += 16) {
+            h2f16(vr + d, vf);
+            for (int j = 0; j < 16; ++j) o[d + j] += p * vf[j];
+          }
+          for (; d < D; ++d) o[d] += p * h2f(vr[d]);
         }
       }
     }

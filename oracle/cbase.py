@@ -18,7 +18,80 @@ from pathlib import Path
 import numpy as np
 
 HERE = Path(__file__).resolve().parent
-LIB = HERE / "_lib" / "liboracle_cpu.so"
+LIB_AVX2 = HERE / "_lib" / "liboracle_cpu.so"
+LIB_AVX512 = HERE / "_lib" / "liboracle_cpu_avx512.so"
+_V4_FLAGS = {"avx512f", "avx512bw", "avx512cd", "avx512dq", "avx512vl"}  # what -march=x86-64-v4 assumes
+
+
+def cpu_flags() -> set[str]:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("flags"):
+                return set(line.split(":", 1)[1].split())
+    except OSError:
+        pass
+    return set()
+
+
+def library_path() -> Path:
+    """The AVX-512 build when the host has every x86-64-v4 feature, else the AVX2 build."""
+    return LIB_AVX512 if _V4_FLAGS <= cpu_flags() else LIB_AVX2
+
+
+def host_info() -> dict:
+    """Facts about the host the CPU baseline ran on: logical CPUs, the lscpu model name, the ISA build used."""
+    model = ""
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.strip().lower().startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except (OSError, subprocess.SubprocessError):
+        pass
+    if not model:
+        try:
+            for line in Path("/proc/cpuinfo").read_text().splitlines():
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+        except OSError:
+            pass
+    return {"cpu_model": model, "os_cpu_count": os.cpu_count(), "isa": _isa_name(_chosen or library_path())}
+
+
+def _isa_name(path: Path) -> str:
+    return "avx512 (x86-64-v4)" if path == LIB_AVX512 else "avx2+f16c (x86-64-v3)"
+
+
+_chosen: Path | None = None  # the build time_decode_step picked on this host
+
+
+def choose_fastest_build(m: int, n: int, k: int, log=print) -> dict:
+    """Time one Q4_0 GEMM of [m, k] x [n, k] (best of 2) with each build this host can run and keep the faster
+    for the rest of the process; returns {isa: seconds}."""
+    global _lib, _chosen
+    builds = [LIB_AVX2] + ([LIB_AVX512] if _V4_FLAGS <= cpu_flags() and LIB_AVX512.exists() else [])
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    w = _rand_q4(rng, n, k)
+    times = {}
+    for path in builds:
+        _lib, _chosen = None, path
+        y = np.empty((m, n), np.float32)
+        q4_0_gemm(x, w, n, out=y)  # warm-up
+        best = min(_timed_once(lambda: q4_0_gemm(x, w, n, out=y)) for _ in range(2))
+        times[_isa_name(path)] = best
+    fastest = min(builds, key=lambda p: times[_isa_name(p)])
+    _lib, _chosen = None, fastest
+    log("cpu: build choice " + ", ".join(f"{k} {v * 1e3:.1f} ms" for k, v in times.items()) + f" -> {_isa_name(fastest)}")
+    return times
+
+
+def _timed_once(fn) -> float:
+    t0 = time.perf_counter()
+    fn()
+    return time.perf_counter() - t0
 
 _f = ctypes.POINTER(ctypes.c_float)
 _u8 = ctypes.POINTER(ctypes.c_uint8)
@@ -31,9 +104,10 @@ _lib = None
 def load():
     global _lib
     if _lib is None:
-        if not LIB.exists():
+        path = _chosen or library_path()
+        if not path.exists():
             subprocess.run(["make", "-s", "-C", str(HERE), "cpu"], check=True)
-        lib = ctypes.CDLL(str(LIB))
+        lib = ctypes.CDLL(str(path))
         lib.orc_rmsnorm.argtypes = [_f, _f, _f, ctypes.c_int, ctypes.c_int, ctypes.c_float]
         lib.orc_q4_0_gemm.argtypes = [_f, ctypes.c_int, ctypes.c_int, _u8, ctypes.c_int, _f, ctypes.c_int]
         lib.orc_rope.argtypes = [_f, ctypes.c_int, ctypes.c_int, ctypes.c_int, _i32, _f]
@@ -83,6 +157,7 @@ def _rand_q4(rng, n, k):
 
 
 def time_decode_step(*, batch, ctx, hidden, ffn, heads, kv_heads, vocab, layers, budget_s=12.0, log=print) -> dict:
+    build_times = choose_fastest_build(batch, 2 * ffn, hidden, log=log)
     lib = load()
     rng = np.random.default_rng(0)
     D, Pg = hidden // heads, 16
@@ -150,16 +225,11 @@ def time_decode_step(*, batch, ctx, hidden, ffn, heads, kv_heads, vocab, layers,
     step = layers * t_layer + t_head
     log(f"cpu: layer {t_layer * 1e3:.1f} ms x{n_layer}, head {t_head * 1e3:.1f} ms x{n_head}, "
         f"step {step * 1e3:.1f} ms on {threads} threads")
-    model = ""
-    try:
-        for line in Path("/proc/cpuinfo").read_text().splitlines():
-            if line.startswith("model name"):
-                model = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
+    info = host_info()
+    info["gate_up_gemm_ms_by_build"] = {k: round(v * 1e3, 2) for k, v in build_times.items()}
     return {"value": round(batch / step, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
             "sample": f"one full decoder layer for all {batch} sequences ({n_layer} timed runs) + final norm/lm_head/"
                       f"argmax ({n_head} runs) at the bench shapes, step = {layers} x layer + head",
-            "ms_per_step": round(step * 1e3, 2), "cpu_model": model,
-            "omp_num_threads": os.environ.get("OMP_NUM_THREADS")}
+            "ms_per_step": round(step * 1e3, 2), **info,
+            "omp_num_threads": os.environ.get("OMP_NUM_THREADS"), "openmp_threads_used": threads,
+            "blas_threads": "none (no BLAS: the C kernels are the whole computation)"}

@@ -72,6 +72,29 @@ def measured_traffic(path: str) -> dict | None:
         return None
 
 
+COUNTERS_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                             "qgemm_counters_config5_gateup_m128_config4_m32.txt")
+
+
+def measured_counters(path: str, prefix: str) -> dict | None:
+    """The ``<prefix>_*`` figures (MFMA busy, VALU busy, L1 pending, ...) of one kernel from the committed rocprofv3
+    counter summary; null when the file is absent."""
+    try:
+        out = {}
+        with open(path) as f:
+            for line in f:
+                if ":" in line and not line.lstrip().startswith("#"):
+                    k, v = (x.strip() for x in line.split(":", 1))
+                    if k.startswith(prefix + "_"):
+                        out[k[len(prefix) + 1:]] = float(v)
+        if not out:
+            return None
+        out["source"] = os.path.relpath(path, os.path.dirname(os.path.abspath(__file__)))
+        return out
+    except (OSError, ValueError):
+        return None
+
+
 def parse() -> argparse.Namespace:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -486,7 +509,8 @@ def main() -> int:
         "roofline_gemm": {"bound": "hbm", "kernel": f"Q4_0 gate|up GEMM + SwiGLU m={B} (qgemm_xs_kernel, EPI=1)",
                           "achieved": round(gemm_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                           "frac": round(gemm_gbs / HBM_PEAK_GBS, 4), "bytes_per_launch": gemm_bytes,
-                          "us_per_launch": round(gemm_us, 3)},
+                          "us_per_launch": round(gemm_us, 3),
+                          "counters": measured_counters(COUNTERS_FILE, "xs_swiglu")},
         "roofline_gemv": {"bound": "hbm", "kernel": "Q4_0 projections, BASELINE config 3 (n x k, y = x W^T): dequant "
                                                     "GEMV at m <= 8, MFMA GEMM at m = 32",
                           "peak": HBM_PEAK_GBS, "unit": "GB/s", "shapes": gemv},
@@ -495,7 +519,7 @@ def main() -> int:
                                             "BASELINE config 5 shape (n 37888, k 3584)",
                                   "achieved": round(tflops5, 1), "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
                                   "frac": round(tflops5 / MFMA_F16_PEAK_TFLOPS, 4), "us_per_launch": round(us5, 3),
-                                  "hbm_gbs": round(gbs5, 1)},
+                                  "hbm_gbs": round(gbs5, 1), "counters": measured_counters(COUNTERS_FILE, "xl")},
         "step_bytes": {"weights": weight_bytes, "kv": kv_bytes * cfg.num_layers,
                        "hbm_floor_ms": round((weight_bytes + kv_bytes * cfg.num_layers) / HBM_PEAK_GBS / 1e6, 4)},
         "decode_batch1": {"ms_per_step": round(ms_b1, 4), "tokens_per_s": round(1000.0 / ms_b1, 2),

@@ -150,6 +150,20 @@ def pack_rows(w: np.ndarray, bits: int) -> tuple[np.ndarray, np.ndarray, np.ndar
     return np.ascontiguousarray(q), np.ascontiguousarray(scales), np.ascontiguousarray(zps)
 
 
+def unpack_rows(packed: np.ndarray, scales: np.ndarray, zero_points: np.ndarray, bits: int, k: int) -> np.ndarray:
+    """``(q - zero_point) * scale`` in fp32 for ``pack_rows`` output: the reference's
+    ``dequantize_packed_weight`` (``quantization.py:74-84``, int4 unpack ``quantization.py:133-139``)."""
+    packed = np.asarray(packed, dtype=np.uint8)
+    if bits == 4:
+        q = np.empty((packed.shape[0], packed.shape[1] * 2), dtype=np.float32)
+        q[:, 0::2] = packed & 0x0F
+        q[:, 1::2] = packed >> 4
+        q = q[:, :k]
+    else:
+        q = packed.astype(np.float32)
+    return (q - zero_points.astype(np.float32)[:, None]) * scales.astype(np.float32)[:, None]
+
+
 def quantize_q4_0(w: np.ndarray) -> np.ndarray:
     """Dense ``[n, k]`` -> GGUF Q4_0 bytes: per block d = m / -8 where m is the value of
     largest magnitude, q = min(15, floor(x/d + 8.5)) (the ggml reference quantizer)."""
@@ -278,6 +292,11 @@ class HipWeightStore:
                 t = self.source.dense_device(spec.key, dtype)
             else:
                 arr = np.array(self.source.dense(spec.key), copy=True, order="C")
+                bits = row_bits(self.quant)
+                if bits and arr.ndim == 2:
+                    # the reference's --quant int4/int8 store hands every 2-D weight out packed and dequantized,
+                    # dense ones (the token embedding) included (cacheir/runtime/cpu.py:28-37)
+                    arr = unpack_rows(*pack_rows(arr.astype(np.float32), bits), bits, arr.shape[1])
                 t = torch.from_numpy(arr).to(self.device).to(dtype)
             self._dense[key] = t.contiguous()
         return self._dense[key]
@@ -285,9 +304,15 @@ class HipWeightStore:
     def is_blocked(self, names: tuple[str, ...]) -> bool:
         """True when `names` run on the quantized MFMA GEMM (GGUF blocks or the reference's row packing)."""
         keys = [self.specs[n].key for n in names]
-        if self.quant in _FMT_OF or row_bits(self.quant):
+        if self.quant in _FMT_OF:
             return True
+        if row_bits(self.quant):
+            # the tiled layout holds whole 128-column quads; a row-packed weight of another width runs dense
+            return all(self._cols(n) % 128 == 0 for n in names)
         return all(self.source.has_blocks(k) for k in keys)
+
+    def _cols(self, name: str) -> int:
+        return int(self.specs[name].tensor_type.shape[1])
 
     def _row_packed(self, names: tuple[str, ...], interleave: bool = False) -> "kernels.QWeight":
         """Per-row asymmetric int4/int8 packing of the concatenated rows of `names` (each row keeps its own scale and
@@ -313,8 +338,16 @@ class HipWeightStore:
     def matmul_weight(self, names: tuple[str, ...]):
         if names in self._packed:
             return self._packed[names]
-        if row_bits(self.quant):
+        if row_bits(self.quant) and self.is_blocked(names):
             self._packed[names] = self._row_packed(names)
+            return self._packed[names]
+        if row_bits(self.quant):
+            # k is not a multiple of 128 (e.g. the tiny model's ffn 688): the reference's own packed values,
+            # dequantized exactly ((q - zero_point) * scale in fp32, as its runtime does at load), on the fp32 GEMM
+            bits = row_bits(self.quant)
+            dense = [unpack_rows(*pack_rows(np.asarray(self.source.dense(self.specs[n].key), np.float32), bits), bits,
+                                 self._cols(n)) for n in names]
+            self._packed[names] = torch.from_numpy(np.ascontiguousarray(np.concatenate(dense))).to(self.device)
             return self._packed[names]
         if self.is_blocked(names):
             parts, fmt, k = [], None, None

@@ -19,7 +19,7 @@ import pytest
 
 from cacheir_amd import CompileArtifact, retarget
 from cacheir_amd.compiler import compile_config
-from cacheir_amd.weights import pack_rows
+from cacheir_amd.weights import pack_rows, unpack_rows
 from oracle import quant as oq
 
 GOLDEN = Path(__file__).resolve().parent / "golden"
@@ -36,6 +36,8 @@ def test_row_packing_equals_the_reference_bytes(bits):
     packed, scales, zps = pack_rows(w, bits)
     assert packed.shape == tuple(ref["packed_shape"]) and np.array_equal(packed, ref_packed)
     assert np.array_equal(scales, ref_scales) and np.array_equal(zps, ref_zps)
+    # the weight store's own dequant (used for widths the tiled GEMM cannot hold) gives the reference's floats
+    assert np.array_equal(unpack_rows(packed, scales, zps, bits, w.shape[1]), np.asarray(ref["dequant"], np.float32))
     o = oq.asymmetric_pack(w, bits)
     assert np.array_equal(o["packed_values"], ref_packed)
     assert np.array_equal(o["scales"], ref_scales) and np.array_equal(o["zero_points"], ref_zps)

@@ -270,8 +270,10 @@ def test_reference_row_packed_model_matches_oracle(tmp_path, device, quant_name)
     bits = 4 if "4" in quant_name else 8
     decoded = {}
     for k, v in w.items():
-        if v.ndim == 2 and "embed" not in k:
+        if v.ndim == 2:  # every 2-D weight, the embedding table too (cacheir/runtime/cpu.py:28-37)
             decoded[k] = oq.asymmetric_dequant(oq.asymmetric_pack(v, bits))
+            if "embed" in k:  # held as fp16 on the device, like every dense weight of an fp16 runtime
+                decoded[k] = decoded[k].astype(np.float16).astype(np.float32)
         else:
             decoded[k] = v.astype(np.float16).astype(np.float32)
     path = write_model(tmp_path / "m", cfg, w)

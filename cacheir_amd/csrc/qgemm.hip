@@ -39,37 +39,39 @@
 namespace cir {
 namespace {
 
-// (a & m) | c in one v_and_or_b32 (the compiler otherwise emits v_and + v_or with literals).
-__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t c) {
-  uint32_t r;
-  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(m), "v"(c));
-  return r;
-}
-
 __device__ __forceinline__ f16x2 as_h2(uint32_t v) { return __builtin_bit_cast(f16x2, v); }
 
-// 8 Q4_0 nibbles of one dword -> 8 exact fp16 integers (q - 8).
+// 8 Q4_0 nibbles of one dword -> 8 fp16 values (q - 8) * 2^-12, all exact.  A nibble q
+// masked in place reads as the fp16 subnormal q * 2^-24 (16q * 2^-24 for the high nibble
+// of a byte); one packed FMA scales it by 2^12 (2^8) and subtracts 8 * 2^-12.  That is two
+// VALU ops per pair, as many as an or-in of the exponent 1024 would need with one
+// v_and_or_b32, which the compiler does not form from two literal masks.  The kernels'
+// fp16 denormal mode (float_denorm_mode_16_64 = 3, the default) keeps the subnormals.
 __device__ __forceinline__ f16x8 dq_q4(uint32_t w) {
-  const f16x2 c1032 = {(f16)-1032.0f, (f16)-1032.0f};
-  const f16x2 c72 = {(f16)-72.0f, (f16)-72.0f};
-  const f16x2 s16 = {(f16)0.0625f, (f16)0.0625f};
+  const f16x2 s12 = {(f16)4096.0f, (f16)4096.0f};
+  const f16x2 s8 = {(f16)256.0f, (f16)256.0f};
+  const f16x2 c8 = {(f16)-0.001953125f, (f16)-0.001953125f};  // -8 * 2^-12
   const uint32_t t = w >> 8;
-  const f16x2 p0 = as_h2(and_or(w, 0x000F000Fu, 0x64006400u)) + c1032;
-  const f16x2 p1 = as_h2(and_or(w, 0x00F000F0u, 0x64006400u)) * s16 + c72;
-  const f16x2 p2 = as_h2(and_or(t, 0x000F000Fu, 0x64006400u)) + c1032;
-  const f16x2 p3 = as_h2(and_or(t, 0x00F000F0u, 0x64006400u)) * s16 + c72;
+  const f16x2 p0 = as_h2(w & 0x000F000Fu) * s12 + c8;
+  const f16x2 p1 = as_h2(w & 0x00F000F0u) * s8 + c8;
+  const f16x2 p2 = as_h2(t & 0x000F000Fu) * s12 + c8;
+  const f16x2 p3 = as_h2(t & 0x00F000F0u) * s8 + c8;
   return f16x8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
 }
 
-// 8 Q8_0 int8 values (two dwords) -> 8 exact fp16 integers q.
+// 8 Q8_0 int8 values (two dwords) -> 8 exact fp16 integers q.  After the sign flip each
+// byte is q + 128; one v_perm_b32 places bytes 0 and 2 (or 1 and 3) under 0x64 bytes,
+// giving fp16 1024 + q + 128.  Byte selectors 4..7 pick bytes 0..3 of the first
+// operand, 0..3 those of the second.
 __device__ __forceinline__ f16x8 dq_q8(uint32_t w0, uint32_t w1) {
   const f16x2 c1152 = {(f16)-1152.0f, (f16)-1152.0f};
+  constexpr uint32_t k64 = 0x64646464u, even = 0x00060004u, odd = 0x00070005u;
   w0 ^= 0x80808080u;
   w1 ^= 0x80808080u;
-  const f16x2 p0 = as_h2(and_or(w0, 0x00FF00FFu, 0x64006400u)) + c1152;
-  const f16x2 p1 = as_h2(and_or(w0 >> 8, 0x00FF00FFu, 0x64006400u)) + c1152;
-  const f16x2 p2 = as_h2(and_or(w1, 0x00FF00FFu, 0x64006400u)) + c1152;
-  const f16x2 p3 = as_h2(and_or(w1 >> 8, 0x00FF00FFu, 0x64006400u)) + c1152;
+  const f16x2 p0 = as_h2(__builtin_amdgcn_perm(w0, k64, even)) + c1152;
+  const f16x2 p1 = as_h2(__builtin_amdgcn_perm(w0, k64, odd)) + c1152;
+  const f16x2 p2 = as_h2(__builtin_amdgcn_perm(w1, k64, even)) + c1152;
+  const f16x2 p3 = as_h2(__builtin_amdgcn_perm(w1, k64, odd)) + c1152;
   return f16x8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
 }
 
@@ -96,6 +98,12 @@ __host__ __device__ constexpr int layout_fmt(int fmt) {
   return (fmt == CIR_Q4_0 || fmt == CIR_I4_ROW) ? CIR_Q4_0 : CIR_Q8_0;
 }
 __host__ __device__ size_t quant_bytes_per_lane(int fmt) { return layout_fmt(fmt) == CIR_Q4_0 ? 16 : 32; }
+
+// Accumulators of a 4-bit layout hold 2^-12 times the dot products (dq_q4's scale); each
+// kernel multiplies them by kAccScale once, when its k range is done.  Scaling by a power
+// of two commutes with every fp32 rounding before it (no value comes near the fp32
+// subnormal range), so the results are the ones integer weights would give.
+template <int FMT> inline constexpr float kAccScale = layout_fmt(FMT) == CIR_Q4_0 ? 4096.f : 1.f;
 __host__ __device__ size_t block_bytes(int fmt) { return fmt == CIR_Q4_0 ? 18 : 34; }
 __host__ __device__ bool valid_fmt(int fmt) {
   return fmt == CIR_Q4_0 || fmt == CIR_Q8_0 || fmt == CIR_I4_ROW || fmt == CIR_I8_ROW;
@@ -263,7 +271,7 @@ struct Stage {
   f16x8 x[MT][4];
 };
 
-// Exact integer weights ((q - 8) for Q4_0, q for Q8_0) feed one MFMA per 32-value
+// Exact weights ((q - 8) * 2^-12 for Q4_0, q for Q8_0) feed one MFMA per 32-value
 // block; the block's fp32 result is scaled by d in fp32 and accumulated.  All MFMAs
 // of a block step are issued before their scale FMAs so the MFMA latency overlaps.
 template <int FMT, int NT, int MT>
@@ -487,6 +495,12 @@ __global__ __launch_bounds__(256 * KG) void qgemm_xs_kernel(const f16* __restric
       barrier();
     }
   });
+  if constexpr (kAccScale<FMT> != 1.f) {
+#pragma unroll
+    for (int a = 0; a < MT; ++a)
+#pragma unroll
+      for (int b = 0; b < NT; ++b) acc[a][b] *= kAccScale<FMT>;
+  }
 
   if constexpr (KG > 1) {
     // The loop ended on a barrier after the last LDS read.  Groups 1.. park their
@@ -775,6 +789,12 @@ __global__ __launch_bounds__(64 * W) void qgemm_xl_kernel(const f16* __restrict_
       barrier();
     }
   });
+  if constexpr (kAccScale<FMT> != 1.f) {
+#pragma unroll
+    for (int a = 0; a < MT; ++a)
+#pragma unroll
+      for (int b = 0; b < NT; ++b) acc[a][b] *= kAccScale<FMT>;
+  }
 
   if constexpr (is_row_fmt(FMT)) {
     const float* rscale = reinterpret_cast<const float*>(wd);
@@ -1001,6 +1021,10 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void qgemv_kernel(const f16* __
   auto store_tile = [&]() __attribute__((always_inline)) {
     const int t = t0 + cl;
     const int n = t * 16 + li;
+    if constexpr (kAccScale<FMT> != 1.f) {
+#pragma unroll
+      for (int r = 0; r < MR; ++r) acc[r] *= kAccScale<FMT>;
+    }
     if constexpr (is_row_fmt(FMT)) {
       // w = (c - zp) * s with c the stored code: acc holds sum x*c over this split,
       // so the split's share of y is s * (acc + (c0 - zp) * sum x), c0 - zp = offset[row].
@@ -1053,13 +1077,6 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void qgemv_kernel(const f16* __
         const f32x4 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(xf[j], wb, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
 #pragma unroll
         for (int r = 0; r < MR; ++r) acc[r] = fmaf(dj, c[r], acc[r]);
-        // Rows MR..3 of c are never read.  Without this use the register allocator may
-        // hand their registers to the next dequant's inline v_and_or_b32 while the MFMA
-        // that writes them is still in flight; no wait is inserted for an inline-asm
-        // writer, so the late MFMA write would clobber the next B operand.  The empty
-        // statement reads all four and is ordered after the FMAs (it "updates" acc),
-        // whose read of the result waits for the MFMA to finish.
-        if constexpr (MR < 4) asm volatile("" : "+v"(acc) : "v"(c));
       }
     }
     if (cq == nq - 1) store_tile();  // uniform

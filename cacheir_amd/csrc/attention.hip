@@ -91,6 +91,7 @@ constexpr int kBlock = 16 * kTiles;   // tokens per wavefront step
 constexpr int kWaves = 8;             // wavefronts per workgroup (fp16 path)
 constexpr int kChunk = 128;  // tokens per partial in the generic path
 constexpr int kPtCache = 512;  // page-table entries a workgroup keeps in LDS (2 KiB)
+static_assert(64 * kWaves <= kPtCache, "one page-table entry per thread");
 constexpr int kMinSplitTokens = 256;
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -115,27 +116,12 @@ struct QkvIn {
   const int32_t* positions; // [batch]: position of the new token
 };
 
-// Sum over the splits in split order (bitwise as the epilogue kernels sum).  Up to
-// kSumUnroll splits every load is issued before the first add (one memory round trip
-// instead of one per split); indices past `splits` re-read split 0 and are dropped.
+// Splits of the QKV partials a fused workgroup loads before its first K/V block;
+// more splits are loaded when summed.
 constexpr int kSumUnroll = 8;
-__device__ __forceinline__ float sum_splits(const float* __restrict__ p, int splits, size_t plane, size_t idx) {
-  if (splits <= kSumUnroll) {
-    float t[kSumUnroll];
-#pragma unroll
-    for (int s = 0; s < kSumUnroll; ++s) t[s] = p[(size_t)(s < splits ? s : 0) * plane + idx];
-    float v = t[0];
-#pragma unroll
-    for (int s = 1; s < kSumUnroll; ++s)
-      if (s < splits) v += t[s];
-    return v;
-  }
-  float v = p[idx];
-  for (int s = 1; s < splits; ++s) v += p[(size_t)s * plane + idx];
-  return v;
-}
 
-template <int G>
+// FUSED: q comes from the QKV partials in `qkv` (decode, q_len 1), else from `q`.
+template <int G, bool FUSED>
 __global__ __launch_bounds__(64 * kWaves) void attn_f16_d128(
     const f16* __restrict__ q, f16* __restrict__ kp, f16* __restrict__ vp,
     const int32_t* __restrict__ pt, const int32_t* __restrict__ lens, f16* __restrict__ out,
@@ -213,74 +199,128 @@ __global__ __launch_bounds__(64 * kWaves) void attn_f16_d128(
     load_k(o, blk);
     load_v(o, blk);
   };
-  // The first block's K/V do not depend on q: issue them before the fused prologue so
-  // its latency overlaps theirs -- except in the wavefront whose block holds the new
-  // token (that one is appended by the prologue).
-  Blk A;
-  int blk = b0 + wave;
-  bool loaded = false;
-  if (qkv.part && blk < b1 && blk != (qkv.positions[b] / kBlock)) {
-    load_block(A, blk);
-    loaded = true;
-  }
-  if (pt_cached)
-    for (int i = threadIdx.x; i < pg1 - pg0; i += 64 * kWaves) sm_pt[i] = ptrow[pg0 + i];
-  if (qkv.part) {  // fused decode input (q_len == 1): q, k, v of this row and KV head
-    const int pos = qkv.positions[b];
-    const int N = (Hq + 2 * Hkv) * D;
-    const size_t plane = (size_t)gridDim.z * N;
-    const float* base = qkv.part + (size_t)row * N;
-    const int page_idx = pos / P;
-    const int slot = (page_idx < max_pages) ? ptrow[page_idx] : -1;
-    const int off = pos - page_idx * P;
-    // The split whose blocks hold the new token appends it (and alone reads it back).
-    const bool writer = split == min(S - 1, (pos / kBlock) / max(per, 1));
-    constexpr int kHalf = D / 2;
-    for (int it = threadIdx.x; it < (G + 1) * kHalf + D; it += 64 * kWaves) {
-      if (it < (G + 1) * kHalf) {  // RoPE pair i of q head hh (hh < G) or of k (hh == G)
-        const int hh = it / kHalf, i = it - hh * kHalf;
-        const size_t col0 = (hh < G ? ((size_t)kvh * G + hh) * D : (size_t)Hq * D + (size_t)kvh * D) + 2 * i;
-        const float x0 = sum_splits(base, qkv.splits, plane, col0);
-        const float x1 = sum_splits(base, qkv.splits, plane, col0 + 1);
-        float sn, cs;
-        sincosf((float)pos * qkv.inv_freq[i], &sn, &cs);
-        const float y0 = x0 * cs - x1 * sn;
-        const float y1 = x0 * sn + x1 * cs;
-        if (hh < G) {
-          sm_q[hh][2 * i] = static_cast<f16>(y0);
-          sm_q[hh][2 * i + 1] = static_cast<f16>(y1);
-        } else if (writer && slot >= 0) {
-          f16* o = kp + (((size_t)slot * Hkv + kvh) * P + off) * D + 2 * i;
-          o[0] = static_cast<f16>(y0);
-          o[1] = static_cast<f16>(y1);
-        }
-      } else {
-        const int d = it - (G + 1) * kHalf;
-        const float v = sum_splits(base, qkv.splits, plane, (size_t)(Hq + Hkv) * D + (size_t)kvh * D + d);
-        if (writer && slot >= 0) vp[(((size_t)slot * Hkv + kvh) * P + off) * D + d] = static_cast<f16>(v);
-      }
-    }
-    // Publishes q and the page-table cache in LDS and the appended k/v (global stores
-    // before a workgroup barrier are visible to the workgroup; no wavefront has read
-    // that page line yet).
-    __syncthreads();
-  } else if (pt_cached) {
-    __syncthreads();  // publishes the page-table cache
-  }
-  pt_ready = true;
-
+  // Issue order: load counters retire in order, so waiting for one load waits for every
+  // load issued before it.  q (or the fused prologue's partials) and the page-table
+  // entries for the LDS cache go out first, the first K/V block after them, and in a
+  // workgroup with blocks every thread issues the same loads (indices clamped, results
+  // unused where out of range), so the compiler's waits before the LDS fill and the
+  // prologue's arithmetic count the block's loads out instead of waiting for them.
+  //
   // Q as the MFMA A operand: row li = head kvh*G + li (zero rows past G); element e
   // of step s is head dim 32*s + 8*lg + e, the same mapping the K loads use.
   f16x8 qa[4];
-  {
-    const f16* qrow = qkv.part ? &sm_q[li < G ? li : 0][8 * lg]
-                               : q + ((size_t)row * Hq + (size_t)kvh * G + (li < G ? li : 0)) * D + 8 * lg;
+  if constexpr (!FUSED) {
+    const f16* qrow = q + ((size_t)row * Hq + (size_t)kvh * G + (li < G ? li : 0)) * D + 8 * lg;
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       const f16x8 v = *reinterpret_cast<const f16x8*>(qrow + 32 * s);
       qa[s] = (li < G) ? v : f16x8{0, 0, 0, 0, 0, 0, 0, 0};
     }
   }
+
+  // Fused decode input: q, k, v of this row and KV head.  Work items are column pairs:
+  // RoPE pair i of q head hh (hh < G) or of k (hh == G), then pairs of v (hh == G + 1).
+  // The split whose blocks hold the new token appends it (and alone reads it back);
+  // the other splits need only q.  The first kSumUnroll splits of an item are loaded
+  // up front; more splits are loaded when the item is summed.
+  constexpr int kHalf = D / 2;
+  constexpr int kItems = ((G + 2) * kHalf + 64 * kWaves - 1) / (64 * kWaves);  // per thread
+  const int pos = FUSED ? qkv.positions[b] : 0;
+  const bool writer = FUSED && split == min(S - 1, (pos / kBlock) / max(per, 1));
+  const int items = writer ? (G + 2) * kHalf : G * kHalf;
+  const int N = (Hq + 2 * Hkv) * D;
+  const size_t plane = (size_t)gridDim.z * N;
+  const float* prow = FUSED ? qkv.part + (size_t)row * N : nullptr;
+  auto item_col = [&](int it) __attribute__((always_inline)) -> size_t {  // first column of item it
+    const int hh = it / kHalf, i = it - hh * kHalf;
+    return (hh < G ? ((size_t)kvh * G + hh) * D : (size_t)(Hq + (hh - G) * Hkv) * D + (size_t)kvh * D) + 2 * i;
+  };
+  float xa[kItems][kSumUnroll], xb[kItems][kSumUnroll], fr[kItems];
+  if constexpr (FUSED) {
+#pragma unroll
+    for (int k = 0; k < kItems; ++k) {
+      const int it = min((int)threadIdx.x + k * 64 * kWaves, items - 1);
+      const float* p = prow + item_col(it);
+#pragma unroll
+      for (int s = 0; s < kSumUnroll; ++s) {
+        const float* ps = p + (size_t)(s < qkv.splits ? s : 0) * plane;
+        xa[k][s] = ps[0];
+        xb[k][s] = ps[1];
+      }
+      fr[k] = qkv.inv_freq[it % kHalf];
+    }
+  }
+  // Sums each item's partials in split order (bitwise as the QKV epilogue kernel), applies RoPE,
+  // keeps q in LDS and appends k and v (writer only).
+  auto prologue = [&]() __attribute__((always_inline)) {
+    const int page_idx = pos / P;
+    const int slot = (writer && page_idx < max_pages) ? ptrow[page_idx] : -1;
+    const int off = pos - page_idx * P;
+    auto sum = [&](const float (&t)[kSumUnroll], size_t col) __attribute__((always_inline)) {
+      float v = t[0];
+#pragma unroll
+      for (int s = 1; s < kSumUnroll; ++s)
+        if (s < qkv.splits) v += t[s];
+      for (int s = kSumUnroll; s < qkv.splits; ++s) v += prow[(size_t)s * plane + col];
+      return v;
+    };
+#pragma unroll
+    for (int k = 0; k < kItems; ++k) {
+      const int it = threadIdx.x + k * 64 * kWaves;
+      if (it >= items) continue;
+      const int hh = it / kHalf, i = it - hh * kHalf;
+      const size_t col = item_col(it);
+      const float x0 = sum(xa[k], col), x1 = sum(xb[k], col + 1);
+      f16x2 y;
+      if (hh <= G) {  // q or k: RoPE
+        float sn, cs;
+        sincosf((float)pos * fr[k], &sn, &cs);
+        // Rounded to fp32 before the fp16 conversion, as the QKV epilogue kernel does.
+        y = f16x2{static_cast<f16>(as_f32_value(x0 * cs - x1 * sn)), static_cast<f16>(as_f32_value(x0 * sn + x1 * cs))};
+      } else {
+        y = f16x2{static_cast<f16>(x0), static_cast<f16>(x1)};
+      }
+      if (hh < G) {
+        *reinterpret_cast<f16x2*>(&sm_q[hh][2 * i]) = y;
+      } else if (slot >= 0) {  // one dword per pair: a wavefront writes whole rows
+        f16* pool = hh == G ? kp : vp;
+        *reinterpret_cast<f16x2*>(pool + (((size_t)slot * Hkv + kvh) * P + off) * D + 2 * i) = y;
+      }
+    }
+  };
+
+  // The first block's K/V do not depend on q: issue them before the workgroup barrier
+  // and the fused prologue's arithmetic.  A wavefront without a block of its own loads
+  // block b0 and drops it; the one whose block holds the new token of a fused call
+  // loads it again after the barrier (the prologue appends that token).
+  Blk A;
+  int blk = b0 + wave;
+  bool loaded = false;
+  if (b0 < b1) {  // uniform: pg0 .. pg1 - 1 and block b0 exist
+    const int ptv = ptrow[pg0 + min((int)threadIdx.x, pg1 - pg0 - 1)];
+    load_block(A, blk < b1 ? blk : b0);
+    loaded = blk < b1 && !(FUSED && blk == pos / kBlock);
+    // Every thread writes (entries past the split's pages are never read): a store under
+    // a condition would let the compiler sink the load below the block's loads.
+    sm_pt[threadIdx.x] = ptv;
+    if constexpr (FUSED) prologue();
+  } else if (writer) {
+    prologue();
+  }
+  if constexpr (FUSED) {
+    // Publishes q and the page-table cache in LDS and the appended k/v (global stores
+    // before a workgroup barrier are visible to the workgroup; no wavefront has read
+    // that page line yet).
+    __syncthreads();
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const f16x8 v = *reinterpret_cast<const f16x8*>(&sm_q[li < G ? li : 0][8 * lg + 32 * s]);
+      qa[s] = (li < G) ? v : f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+    }
+  } else if (pt_cached) {
+    __syncthreads();  // publishes the page-table cache
+  }
+  pt_ready = true;
 
   float m[4], lsum[4];
 #pragma unroll
@@ -645,8 +685,12 @@ int launch_attention(const void* q, const void* k_pool, const void* v_pool, cons
     auto ko = static_cast<f16*>(out);
 #define CIR_ATT_CASE(g)                                                                                             \
   case g:                                                                                                           \
-    attn_f16_d128<g><<<grid, 64 * kWaves, 0, s>>>(kq, kk, kv, page_table, seq_lens, ko, part_o, part_ml, q_len, Hq, \
-                                                  Hkv, P, max_pages, S, scale_log2, qkv);                           \
+    if (qkv.part)                                                                                                   \
+      attn_f16_d128<g, true><<<grid, 64 * kWaves, 0, s>>>(kq, kk, kv, page_table, seq_lens, ko, part_o, part_ml,   \
+                                                           q_len, Hq, Hkv, P, max_pages, S, scale_log2, qkv);      \
+    else                                                                                                            \
+      attn_f16_d128<g, false><<<grid, 64 * kWaves, 0, s>>>(kq, kk, kv, page_table, seq_lens, ko, part_o, part_ml,  \
+                                                            q_len, Hq, Hkv, P, max_pages, S, scale_log2, qkv);     \
     break;
     switch (G) {
       CIR_ATT_CASE(1) CIR_ATT_CASE(2) CIR_ATT_CASE(3) CIR_ATT_CASE(4)

@@ -126,7 +126,7 @@ __global__ __launch_bounds__(64 * kWaves) void attn_f16_d128(
     const f16* __restrict__ q, f16* __restrict__ kp, f16* __restrict__ vp,
     const int32_t* __restrict__ pt, const int32_t* __restrict__ lens, f16* __restrict__ out,
     float* __restrict__ part_o, float* __restrict__ part_ml, int q_len, int Hq, int Hkv, int P, int max_pages,
-    int S, float scale_log2, QkvIn qkv) {
+    int S, float scale_log2, int sort_rows, QkvIn qkv) {
   constexpr int D = 128;
   __shared__ float sm_m[kWaves][16];
   __shared__ float sm_l[kWaves][16];
@@ -134,7 +134,30 @@ __global__ __launch_bounds__(64 * kWaves) void attn_f16_d128(
   __shared__ __align__(16) f16 sm_q[G][D];
   __shared__ int sm_pt[kPtCache];
 
-  const int split = blockIdx.x, kvh = blockIdx.y, row = blockIdx.z;
+  const int split = blockIdx.x, kvh = blockIdx.y;
+  // Rows in decreasing order of context (sort_rows: decode, rows <= one per thread, more
+  // workgroups than CUs): workgroups are dispatched in blockIdx order as CUs free up,
+  // so the longest rows start first and the short ones fill in behind them (longest
+  // processing time first) instead of a long row starting last and running alone.
+  // Row t's rank counts the rows longer than it, ties broken by index.
+  int row = blockIdx.z;
+  if (sort_rows) {
+    const int n = gridDim.z, t = threadIdx.x;
+    const int lt = t < n ? lens[t] : 0;
+    sm_pt[t] = lt;  // (the page-table cache is filled later)
+    __syncthreads();
+    if (t < n) {
+      int rank = 0;
+      for (int j = 0; j < n; ++j) {
+        const int lj = sm_pt[j];
+        rank += (lj > lt || (lj == lt && j < t)) ? 1 : 0;
+      }
+      if (rank == (int)blockIdx.z) sm_m[0][0] = __builtin_bit_cast(float, t);
+    }
+    __syncthreads();
+    row = __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, sm_m[0][0]));
+    __syncthreads();  // sm_pt and sm_m are written again below
+  }
   // readfirstlane: the wavefront index is uniform, so block indices and page-table
   // lookups stay scalar (s_load, their own counter) instead of vector loads that
   // would retire in order behind the K/V loads in flight.
@@ -645,6 +668,19 @@ size_t partial_bytes(int rows, int Hq, int D, int S, bool mfma) {
   return (size_t)rows * Hq * S * ((size_t)D + 2) * sizeof(float);
 }
 
+// Compute units of the current device, looked up once per device.
+int device_cus() {
+  static std::atomic<int> cus[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int n = cus[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cus[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
 int launch_attention(const void* q, const void* k_pool, const void* v_pool, const int32_t* page_table,
                      const int32_t* seq_lens, void* out, void* workspace, size_t workspace_bytes,
                      int batch, int q_len, int Hq, int Hkv, int D, int P, int max_pages, float scale,
@@ -679,6 +715,8 @@ int launch_attention(const void* q, const void* k_pool, const void* v_pool, cons
   float* part_ml = part_o + (size_t)rows * Hq * S * D;
   dim3 grid(S, Hkv, rows);
   if (mfma) {
+    // Longest rows first when the workgroups outnumber the CUs (they then run in rounds).
+    const int sort_rows = q_len == 1 && rows <= 64 * kWaves && (long)S * Hkv * rows > device_cus();
     auto kq = static_cast<const f16*>(q);
     auto kk = static_cast<f16*>(const_cast<void*>(k_pool));
     auto kv = static_cast<f16*>(const_cast<void*>(v_pool));
@@ -687,10 +725,12 @@ int launch_attention(const void* q, const void* k_pool, const void* v_pool, cons
   case g:                                                                                                           \
     if (qkv.part)                                                                                                   \
       attn_f16_d128<g, true><<<grid, 64 * kWaves, 0, s>>>(kq, kk, kv, page_table, seq_lens, ko, part_o, part_ml,   \
-                                                           q_len, Hq, Hkv, P, max_pages, S, scale_log2, qkv);      \
+                                                           q_len, Hq, Hkv, P, max_pages, S, scale_log2,          \
+                                                           sort_rows, qkv);                                        \
     else                                                                                                            \
       attn_f16_d128<g, false><<<grid, 64 * kWaves, 0, s>>>(kq, kk, kv, page_table, seq_lens, ko, part_o, part_ml,  \
-                                                            q_len, Hq, Hkv, P, max_pages, S, scale_log2, qkv);     \
+                                                            q_len, Hq, Hkv, P, max_pages, S, scale_log2,         \
+                                                            sort_rows, qkv);                                       \
     break;
     switch (G) {
       CIR_ATT_CASE(1) CIR_ATT_CASE(2) CIR_ATT_CASE(3) CIR_ATT_CASE(4)

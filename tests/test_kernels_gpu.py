@@ -90,6 +90,27 @@ def test_attention_empty_sequence_gives_zeros(device):
     close16(out[1], paged.paged_attention(q[1:], kp, vp, pt[1:], lens[1:], 8, 2)[0])
 
 
+@pytest.mark.parametrize("hq,hkv", [(32, 8), (28, 4)])
+def test_attention_rows_dispatched_longest_first(device, hq, hkv):
+    """More (row, KV head) workgroups than CUs: the kernel reorders rows by decreasing context
+    (ties by index) before dispatch.  Ties, empty rows and single tokens still land in their own rows."""
+    from cacheir_amd import kernels
+
+    rng = np.random.default_rng(hkv)
+    batch = 512 // hkv + 8
+    ctx = rng.choice([0, 1, 31, 32, 33, 200, 200, 513, 900], batch).astype(np.int64)
+    kp, vp, pt, lens = paged.build_pool(rng, np.maximum(ctx, 1), hkv, 128, 16)
+    lens = ctx.astype(np.int32)
+    assert batch * hkv > 256
+    q = rng.standard_normal((batch, hq, 128)).astype(np.float16)
+    out = kernels.paged_decode_attention(to_dev(q, device), to_dev(kp, device), to_dev(vp, device), to_dev(pt, device),
+                                         to_dev(lens, device), check_tables=True).float().cpu().numpy()
+    live = lens > 0
+    assert np.all(out[~live] == 0)
+    ref = paged.paged_attention(q[live], kp, vp, pt[live], lens[live], hq, hkv)
+    close16(out[live], ref)
+
+
 def test_attention_config2_full_size(device):
     """B=64, Hq 32 / Hkv 8, D 128, ctx U[512,4096], P 16, permuted pool."""
     from cacheir_amd import kernels
@@ -292,10 +313,12 @@ def test_epilogue_qkv_rope_append(device, kvdt):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("batch,hq,hkv,splits", [(32, 32, 8, 3), (2, 32, 8, 1), (5, 28, 4, 2), (3, 8, 8, 1)])
+@pytest.mark.parametrize("batch,hq,hkv,splits", [(32, 32, 8, 3), (2, 32, 8, 1), (5, 28, 4, 2), (3, 8, 8, 1),
+                                                 (96, 28, 4, 2)])
 def test_fused_qkv_decode_attention_matches_epilogue_then_attention(device, batch, hq, hkv, splits):
     """cir_paged_decode_attention_qkv == cir_epilogue_qkv_rope_append + cir_paged_decode_attention, bitwise:
-    attention output and the pool contents (the appended k/v), incl. small batches that split the context."""
+    attention output and the pool contents (the appended k/v), incl. small batches that split the context and
+    (96 rows x 4 KV heads: more workgroups than CUs) rows dispatched longest first."""
     from cacheir_amd import kernels
 
     rng = np.random.default_rng(batch * 100 + hq)

@@ -29,7 +29,8 @@ __global__ void embedding_kernel(const int64_t* __restrict__ ids, const TT* __re
                                  int hidden, int vocab) {
   const int r = blockIdx.x;
   int64_t id = ids[r];
-  // Out-of-range ids are clamped (the reference would raise IndexError on the host).
+  // Out-of-range ids are clamped, so no id reads outside the table; the runtime
+  // rejects them on the host before they get here.
   id = id < 0 ? 0 : (id >= vocab ? vocab - 1 : id);
   const TT* src = table + (size_t)id * hidden;
   TO* dst = out + (size_t)r * hidden;

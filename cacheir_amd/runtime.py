@@ -688,6 +688,10 @@ class HipRuntime:
     def _prepare(self, caches: list[HipPagedKVCache], ids: np.ndarray, mode: str) -> "StepPlan":
         """Reserve and map the KV pages the step writes, and load the step inputs into its plan."""
         batch, q_len = ids.shape
+        if ids.size and (int(ids.min()) < 0 or int(ids.max()) >= self.config.vocab_size):
+            bad = int(ids.min()) if int(ids.min()) < 0 else int(ids.max())
+            # the reference's embedding lookup raises IndexError (cpu.py:223-224)
+            raise IndexError(f"token id {bad} is out of range for vocabulary size {self.config.vocab_size}")
         P = self.kv_allocator.page_size
         need_pages = sum(max(0, -(-(c.tokens + q_len) // P) - len(c.slots)) for c in caches)
         self.kv_allocator.reserve(need_pages)  # grow (and re-base pools) before any plan is built

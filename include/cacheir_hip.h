@@ -52,6 +52,11 @@ const char* cir_last_error_string(void);
  * k_pool   [slots, num_kv_heads, page_size, head_dim] (kv_dtype), v_pool likewise
  * page_table [batch, max_pages] int32 slot ids; seq_lens [batch] int32 (tokens to
  *   attend, the new token included); out [batch, num_heads, head_dim] (kv_dtype).
+ *   Both live on the device and are not read by the host: every entry a sequence
+ *   uses (the first ceil(seq_len / page_size)) must be a slot of the pools, and
+ *   seq_len at most max_pages * page_size (longer contexts are clamped to it).  The
+ *   Python wrappers check this on request (check_tables=True); the runtime builds
+ *   its tables from its own allocator.
  * Head h reads KV head h / (num_heads / num_kv_heads).  scale multiplies q.k
  * (the reference uses 1/sqrt(head_dim)).  A sequence with seq_len 0 yields zeros.
  * fp16 path: head_dim 128 (MFMA); fp32 path: any head_dim <= 256. */
@@ -245,7 +250,10 @@ int cir_epilogue_qkv_rope_append(const float* y_partial, int splits, const float
 
 /* ------------------------------------------------------------- row kernels ---
  * Token embedding gather (cpu.py:223-224): out[r][:] = table[ids[r]][:]; table
- * dtype tdt, out dtype odt; ids int64. */
+ * dtype tdt, out dtype odt; ids int64.  The ids live on the device, so the call
+ * cannot reject them: an id outside [0, vocab) reads row 0 or vocab - 1.  Callers
+ * validate ids on the host (the runtime raises IndexError, as the reference's
+ * table lookup does). */
 int cir_embedding(const int64_t* ids, const void* table, int tdt, void* out, int odt,
                   int rows, int hidden, int vocab, void* stream);
 

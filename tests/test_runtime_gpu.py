@@ -137,6 +137,23 @@ def test_batch_validation_errors(tiny):
     other = HipRuntime(art, dtype="float32")  # separate allocator
     with pytest.raises(ValueError):
         rt.run_decode_batch([rt, other], [1, 1])
+    # token ids outside the vocabulary raise IndexError on the host, as the reference's table lookup does, and
+    # leave the session untouched (the device embedding would otherwise clamp them)
+    vocab = art.config.vocab_size
+    rt.run([1, 2, 3], mode="prefill")
+    held = rt.kv_cache.tokens
+    for bad in (vocab, -1):
+        with pytest.raises(IndexError):
+            rt.run([[bad]], mode="decode")
+        with pytest.raises(IndexError):
+            rt.run_decode_batch([rt], [bad])
+        with pytest.raises(IndexError):
+            rt.decode_greedy([rt], [bad])
+    with pytest.raises(IndexError):
+        rt.run([5, vocab + 7, 6], mode="prefill", reset_kv=False)
+    assert rt.kv_cache.tokens == held
+    rt.run([[vocab - 1]], mode="decode")  # the largest id is fine
+    assert rt.kv_cache.tokens == held + 1
 
 
 def _q4_model(tmp: Path, fmt: str):

@@ -456,6 +456,14 @@ def main() -> int:
     # ---- the same decode step at batch 1 (sequence 0's context): QKV, O, down and the greedy head run the GEMV ----
     plan1 = base.plan("decode", 1, 1, max_pages)
     plan1.set_inputs(ids[:1], rows[:1], np.full(1, ctx - 1, np.int32))
+    plan1.launch_with_argmax()  # the same checks as the batch-B plan: finite logits, fused head == argmax
+    torch.cuda.synchronize()
+    assert torch.isfinite(plan1.logits).all().item(), "non-finite logits at batch 1"
+    want1 = plan1.next_ids.clone()
+    plan1.next_ids.zero_()
+    plan1.launch_greedy()
+    torch.cuda.synchronize()
+    assert torch.equal(plan1.next_ids, want1), "fused greedy head disagrees with argmax(logits) at batch 1"
     ms_b1 = time_greedy_steps(plan1, args.steps, args.warmup)
     kv_b1 = 2 * Hkv * D * 2 * ctx * cfg.num_layers
     log(f"batch-1 step {ms_b1:.3f} ms -> {1000.0 / ms_b1:.1f} tok/s")

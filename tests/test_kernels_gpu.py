@@ -314,11 +314,12 @@ def test_epilogue_qkv_rope_append(device, kvdt):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("batch,hq,hkv,splits", [(32, 32, 8, 3), (2, 32, 8, 1), (5, 28, 4, 2), (3, 8, 8, 1),
-                                                 (96, 28, 4, 2)])
+                                                 (96, 28, 4, 2), (4, 32, 8, 12)])
 def test_fused_qkv_decode_attention_matches_epilogue_then_attention(device, batch, hq, hkv, splits):
     """cir_paged_decode_attention_qkv == cir_epilogue_qkv_rope_append + cir_paged_decode_attention, bitwise:
-    attention output and the pool contents (the appended k/v), incl. small batches that split the context and
-    (96 rows x 4 KV heads: more workgroups than CUs) rows dispatched longest first."""
+    attention output and the pool contents (the appended k/v), incl. small batches that split the context,
+    (96 rows x 4 KV heads: more workgroups than CUs) rows dispatched longest first, and 12 QKV splits (more than
+    the kernel loads ahead of the first K/V block: the rest are loaded when summed)."""
     from cacheir_amd import kernels
 
     rng = np.random.default_rng(batch * 100 + hq)

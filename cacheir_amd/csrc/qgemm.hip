@@ -1233,10 +1233,12 @@ bool gemv_head_fits(int fmt, int m, int k) { return !is_row_fmt(fmt) && gemv_fit
 #endif
 
 // k-groups per workgroup: m > 16 only, and a divisor of the split's quad count.
+// Two where a split has 32 quads or more (measured: the unsplit gate|up and lm_head
+// at k = 4096 gain ~4%; splits of 4-14 quads lose with half as many per group).
 // qgemm (splits 1) and the fused SwiGLU pick the same value for the same k, so
 // their sums run in the same order.
 int xs_kgroups(int m, int quads) {
-  int kg = m > 16 ? CIR_XS_KG : 1;
+  int kg = m > 16 ? (quads >= 32 ? 2 : CIR_XS_KG) : 1;
   while (kg > 1 && quads % kg) kg /= 2;
   return kg;
 }

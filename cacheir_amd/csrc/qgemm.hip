@@ -1232,13 +1232,13 @@ bool gemv_head_fits(int fmt, int m, int k) { return !is_row_fmt(fmt) && gemv_fit
 #define CIR_XS_KG 1
 #endif
 
-// k-groups per workgroup: m > 16 only, and a divisor of the split's quad count.
-// Two where a split has 32 quads or more (measured: the unsplit gate|up and lm_head
-// at k = 4096 gain ~4%; splits of 4-14 quads lose with half as many per group).
-// qgemm (splits 1) and the fused SwiGLU pick the same value for the same k, so
-// their sums run in the same order.
+// k-groups per workgroup: a divisor of the split's quad count.  Two where a split
+// has 32 quads or more, at any m (measured: the unsplit gate|up + SwiGLU at k = 4096
+// gains ~4% at m = 32 and ~10% at m = 1; splits of 4-14 quads lose with half as many
+// per group).  Every epilogue of this kernel (partials, SwiGLU, argmax) picks the
+// same value for the same m and k, so their sums run in the same order.
 int xs_kgroups(int m, int quads) {
-  int kg = m > 16 ? (quads >= 32 ? 2 : CIR_XS_KG) : 1;
+  int kg = quads >= 32 ? 2 : (m > 16 ? CIR_XS_KG : 1);
   while (kg > 1 && quads % kg) kg /= 2;
   return kg;
 }
@@ -1321,7 +1321,7 @@ void launch_qgemm_argmax(const f16* x, int ldx, const uint8_t* wq, const uint16_
     qgemm_xs_kernel<FMT, NT, MT, (MT == 1 ? 4 : CIR_XS_DW), 2, float, KG>
         <<<grid, 256 * KG, 0, s>>>(x, ldx, wq, wd, cand_v, M, N, K, quads, reinterpret_cast<float*>(cand_i));
   };
-  const int kg = MT == 1 ? 1 : xs_kgroups(M, quads);
+  const int kg = xs_kgroups(M, quads);
   if constexpr (CIR_XS_KG >= 4) {
     if (kg == 4) return go.template operator()<4>(), argmax_cand_kernel<<<M, 256, 0, s>>>(cand_v, cand_i, (int)grid.x * 4, M, ids);
   }
@@ -1340,15 +1340,11 @@ void launch_qgemm_xs(const f16* x, int ldx, const uint8_t* wq, const uint16_t* w
     qgemm_xs_kernel<FMT, NT, MT, DW, 0, float, KG><<<grid, 256 * KG, 0, s>>>(x, ldx, wq, wd, part, M, N, K, quads);
   };
   const int kg = xs_kgroups(M, quads);
-  if constexpr (MT == 1) {
-    go.template operator()<1>();
-  } else {
-    if constexpr (CIR_XS_KG >= 4) {
-      if (kg == 4) return go.template operator()<4>();
-    }
-    if (kg == 2) go.template operator()<2>();
-    else go.template operator()<1>();
+  if constexpr (CIR_XS_KG >= 4) {
+    if (kg == 4) return go.template operator()<4>();
   }
+  if (kg == 2) go.template operator()<2>();
+  else go.template operator()<1>();
 }
 
 // Large m: activation rows per workgroup (16 * MT).

@@ -429,11 +429,13 @@ def test_o_projection_from_attention_parts(device, fmt, lens, hq, hkv, want_s):
 @pytest.mark.gpu
 @pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
 @pytest.mark.parametrize("m,k", [(1, 512), (8, 512), (32, 512), (48, 512), (128, 640), (1, 4096), (3, 4096),
-                                 (8, 4096)])
+                                 (8, 4096), (16, 4096), (32, 4096)])
 def test_qgemm_swiglu_matches_gemm_then_epilogue(device, fmt, m, k):
     """cir_qgemm_swiglu over interleaved gate/up tiles == cir_qgemm (splits 1) + cir_epilogue_swiglu, bitwise,
     and within the fp16 bound of the fp64 oracle. At m <= 8 the reference side runs the GEMV (k = 4096 stages
-    all of an 8-row activation in 64 KiB of LDS), so the two kernels' partials are compared bit for bit too."""
+    all of an 8-row activation in 64 KiB of LDS): with 32 quads or more the fused kernel sums two k-groups (even
+    and odd quads) and then adds them, the GEMV sums the quads in order, so there the outputs agree to one fp16
+    ulp (the fp32 sums differ in rounding only); with fewer quads, bit for bit."""
     from cacheir_amd import kernels
 
     rng = np.random.default_rng(11 + m + k)
@@ -451,7 +453,11 @@ def test_qgemm_swiglu_matches_gemm_then_epilogue(device, fmt, m, k):
     w_il = kernels.QWeight.from_blocks(kernels.interleave_gate_up(g_dev, u_dev, inter).reshape(-1), code, 2 * inter, k)
     got = kernels.qgemm_swiglu(xd, w_il, torch.float16)
     torch.cuda.synchronize()
-    assert torch.equal(got, ref)
+    if m <= 8 and k // 128 >= 32:
+        d = (got.float() - ref.float()).abs()
+        assert torch.all(d <= ref.float().abs() * 2.0 ** -10 + 2.0 ** -24), d.max().item()
+    else:
+        assert torch.equal(got, ref)
     xf = x.astype(np.float64)
     g64, u64 = xf @ dec(gate, k).astype(np.float64).T, xf @ dec(up, k).astype(np.float64).T
     want = g64 / (1.0 + np.exp(-g64)) * u64

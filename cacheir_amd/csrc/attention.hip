@@ -132,6 +132,8 @@ __global__ __launch_bounds__(64 * kWaves) void attn_f16_d128(
   __shared__ float sm_l[kWaves][16];
   __shared__ float sm_o[kWaves][G][D];
   __shared__ __align__(16) f16 sm_q[G][D];
+  __shared__ __align__(16) f16 sm_kn[D];  // fused: the new token's k and v
+  __shared__ __align__(16) f16 sm_vn[D];
   __shared__ int sm_pt[kPtCache];
 
   const int split = blockIdx.x, kvh = blockIdx.y;
@@ -243,9 +245,12 @@ __global__ __launch_bounds__(64 * kWaves) void attn_f16_d128(
 
   // Fused decode input: q, k, v of this row and KV head.  Work items are column pairs:
   // RoPE pair i of q head hh (hh < G) or of k (hh == G), then pairs of v (hh == G + 1).
-  // The split whose blocks hold the new token appends it (and alone reads it back);
-  // the other splits need only q.  The first kSumUnroll splits of an item are loaded
-  // up front; more splits are loaded when the item is summed.
+  // The split whose blocks hold the new token (the writer) also computes its k and v:
+  // they go to LDS, the wavefront whose block holds the token patches them into its
+  // registers, and the writer appends them to the pool at the very end (a store
+  // completes after loads issued later and would hold up every wait behind it), so
+  // no ordering between the append and any load of that page line is needed.  The
+  // first kSumUnroll splits of an item are loaded up front; more when it is summed.
   constexpr int kHalf = D / 2;
   constexpr int kItems = ((G + 2) * kHalf + 64 * kWaves - 1) / (64 * kWaves);  // per thread
   const int pos = FUSED ? qkv.positions[b] : 0;
@@ -273,12 +278,9 @@ __global__ __launch_bounds__(64 * kWaves) void attn_f16_d128(
       fr[k] = qkv.inv_freq[it % kHalf];
     }
   }
-  // Sums each item's partials in split order (bitwise as the QKV epilogue kernel), applies RoPE,
-  // keeps q in LDS and appends k and v (writer only).
+  // Sums each item's partials in split order (bitwise as the QKV epilogue kernel),
+  // applies RoPE and puts q (and the writer's k and v) in LDS.
   auto prologue = [&]() __attribute__((always_inline)) {
-    const int page_idx = pos / P;
-    const int slot = (writer && page_idx < max_pages) ? ptrow[page_idx] : -1;
-    const int off = pos - page_idx * P;
     auto sum = [&](const float (&t)[kSumUnroll], size_t col) __attribute__((always_inline)) {
       float v = t[0];
 #pragma unroll
@@ -303,26 +305,19 @@ __global__ __launch_bounds__(64 * kWaves) void attn_f16_d128(
       } else {
         y = f16x2{static_cast<f16>(x0), static_cast<f16>(x1)};
       }
-      if (hh < G) {
-        *reinterpret_cast<f16x2*>(&sm_q[hh][2 * i]) = y;
-      } else if (slot >= 0) {  // one dword per pair: a wavefront writes whole rows
-        f16* pool = hh == G ? kp : vp;
-        *reinterpret_cast<f16x2*>(pool + (((size_t)slot * Hkv + kvh) * P + off) * D + 2 * i) = y;
-      }
+      f16* dst = hh < G ? &sm_q[hh][2 * i] : (hh == G ? &sm_kn[2 * i] : &sm_vn[2 * i]);
+      *reinterpret_cast<f16x2*>(dst) = y;
     }
   };
 
   // The first block's K/V do not depend on q: issue them before the workgroup barrier
   // and the fused prologue's arithmetic.  A wavefront without a block of its own loads
-  // block b0 and drops it; the one whose block holds the new token of a fused call
-  // loads it again after the barrier (the prologue appends that token).
+  // block b0 and drops it.
   Blk A;
   int blk = b0 + wave;
-  bool loaded = false;
   if (b0 < b1) {  // uniform: pg0 .. pg1 - 1 and block b0 exist
     const int ptv = ptrow[pg0 + min((int)threadIdx.x, pg1 - pg0 - 1)];
     load_block(A, blk < b1 ? blk : b0);
-    loaded = blk < b1 && !(FUSED && blk == pos / kBlock);
     // Every thread writes (entries past the split's pages are never read): a store under
     // a condition would let the compiler sink the load below the block's loads.
     sm_pt[threadIdx.x] = ptv;
@@ -331,10 +326,7 @@ __global__ __launch_bounds__(64 * kWaves) void attn_f16_d128(
     prologue();
   }
   if constexpr (FUSED) {
-    // Publishes q and the page-table cache in LDS and the appended k/v (global stores
-    // before a workgroup barrier are visible to the workgroup; no wavefront has read
-    // that page line yet).
-    __syncthreads();
+    __syncthreads();  // publishes q, the new k and v and the page-table cache
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       const f16x8 v = *reinterpret_cast<const f16x8*>(&sm_q[li < G ? li : 0][8 * lg + 32 * s]);
@@ -433,6 +425,35 @@ __global__ __launch_bounds__(64 * kWaves) void attn_f16_d128(
     }
   };
 
+  // Register patch of the new token (fused): every tile whose rows include it -- its
+  // own and any past-the-end tile re-reading the block's first tile -- takes the k row
+  // (lanes li == row) and the v row (lanes lg == row % 4, element row / 4).  Selects,
+  // not conditional writes: registers take no runtime index.
+  auto patch_k = [&](Blk& o, int blk) __attribute__((always_inline)) {
+    const int tb = blk * kBlock;
+#pragma unroll
+    for (int j = 0; j < kTiles; ++j) {
+      const int r = pos - ((tb + 16 * j < L) ? tb + 16 * j : tb);
+      const bool hit = r >= 0 && r < 16 && li == r;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const f16x8 n = *reinterpret_cast<const f16x8*>(&sm_kn[32 * s + 8 * lg]);
+        o.k[j][s] = hit ? n : o.k[j][s];
+      }
+    }
+  };
+  auto patch_v = [&](Blk& o, int blk) __attribute__((always_inline)) {
+    const int tb = blk * kBlock;
+#pragma unroll
+    for (int j = 0; j < kTiles; ++j) {
+      const int r = pos - ((tb + 16 * j < L) ? tb + 16 * j : tb);
+      const bool hit = r >= 0 && r < 16 && lg == (r & 3);
+      const f16x8 n = *reinterpret_cast<const f16x8*>(&sm_vn[8 * li]);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) o.v[j][u] = (hit && u == (r >> 2)) ? n : o.v[j][u];
+    }
+  };
+
   // Rotating pipeline: the next block's K is loaded into the K registers as soon as
   // this block's scores have read them, and its V once P V has read this block's V,
   // so every wavefront keeps loads in flight while it computes.  The last block is
@@ -441,15 +462,24 @@ __global__ __launch_bounds__(64 * kWaves) void attn_f16_d128(
   {
     const int nb = blk < b1 ? (b1 - blk + kWaves - 1) / kWaves : 0;
     if (nb > 0) {
-      if (!loaded) load_block(A, blk);
+      // The block holding a fused call's new token (its wavefront in the writer split):
+      // its k and v rows are patched into the registers.
+      const int blk_new = pos / kBlock;
+      const int patch_blk = (writer && blk_new >= b0 && blk_new < b1 && (blk_new - b0) % kWaves == wave) ? blk_new : -1;
       f32x4 sc[kTiles];
       for (int t = 0; t + 1 < nb; ++t, blk += kWaves) {
+        if (blk == patch_blk) patch_k(A, blk);
         scores(A, blk, sc);
         load_k(A, blk + kWaves);
         __builtin_amdgcn_sched_barrier(0);
+        if (blk == patch_blk) patch_v(A, blk);
         softmax_pv(A, sc);
         load_v(A, blk + kWaves);
         __builtin_amdgcn_sched_barrier(0);
+      }
+      if (blk == patch_blk) {
+        patch_k(A, blk);
+        patch_v(A, blk);
       }
       scores(A, blk, sc);
       softmax_pv(A, sc);
@@ -502,6 +532,15 @@ __global__ __launch_bounds__(64 * kWaves) void attn_f16_d128(
         ml[0] = M;
         ml[1] = den;
       }
+    }
+  }
+  if (writer && (int)threadIdx.x < kHalf) {  // the KV append (fused): k and v pair t, whole rows
+    const int page_idx = pos / P;
+    const int slot = page_idx < max_pages ? ptrow[page_idx] : -1;
+    if (slot >= 0) {
+      const size_t at = (((size_t)slot * Hkv + kvh) * P + (pos - page_idx * P)) * D + 2 * threadIdx.x;
+      *reinterpret_cast<uint32_t*>(kp + at) = *reinterpret_cast<const uint32_t*>(&sm_kn[2 * threadIdx.x]);
+      *reinterpret_cast<uint32_t*>(vp + at) = *reinterpret_cast<const uint32_t*>(&sm_vn[2 * threadIdx.x]);
     }
   }
 }

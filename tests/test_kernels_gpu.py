@@ -90,6 +90,31 @@ def test_attention_empty_sequence_gives_zeros(device):
     close16(out[1], paged.paged_attention(q[1:], kp, vp, pt[1:], lens[1:], 8, 2)[0])
 
 
+@pytest.mark.parametrize("seed", range(10))
+def test_attention_fp16_random_shapes(device, seed):
+    """Seeded sweep of the fp16 MFMA decode attention against the oracle: batch 1-48, every GQA ratio 1-8,
+    1-8 KV heads, pages of 16 or 32 tokens, contexts 0-1300 with block and page edges (1, 31-33, 255-257)
+    mixed in, so split counts, empty rows, partial tiles and the longest-first dispatch all vary."""
+    from cacheir_amd import kernels
+
+    rng = np.random.default_rng(1000 + seed)
+    batch = int(rng.integers(1, 49))
+    g = int(rng.integers(1, 9))
+    hkv = int(rng.choice([1, 2, 4, 8]))
+    psize = int(rng.choice([16, 32]))
+    edges = np.array([0, 1, 31, 32, 33, 255, 256, 257])
+    ctx = np.where(rng.random(batch) < 0.3, rng.choice(edges, batch), rng.integers(0, 1301, batch))
+    kp, vp, pt, _ = paged.build_pool(rng, np.maximum(ctx, 1), hkv, 128, psize)
+    lens = ctx.astype(np.int32)
+    q = rng.standard_normal((batch, g * hkv, 128)).astype(np.float16)
+    out = kernels.paged_decode_attention(to_dev(q, device), to_dev(kp, device), to_dev(vp, device), to_dev(pt, device),
+                                         to_dev(lens, device), check_tables=True).float().cpu().numpy()
+    live = lens > 0
+    assert np.all(out[~live] == 0)
+    if live.any():
+        close16(out[live], paged.paged_attention(q[live], kp, vp, pt[live], lens[live], g * hkv, hkv))
+
+
 @pytest.mark.parametrize("hq,hkv", [(32, 8), (28, 4)])
 def test_attention_rows_dispatched_longest_first(device, hq, hkv):
     """More (row, KV head) workgroups than CUs: the kernel reorders rows by decreasing context
@@ -320,11 +345,31 @@ def test_fused_qkv_decode_attention_matches_epilogue_then_attention(device, batc
     attention output and the pool contents (the appended k/v), incl. small batches that split the context,
     (96 rows x 4 KV heads: more workgroups than CUs) rows dispatched longest first, and 12 QKV splits (more than
     the kernel loads ahead of the first K/V block: the rest are loaded when summed)."""
+    rng = np.random.default_rng(batch * 100 + hq)
+    _fused_equals_two_kernels(device, rng, rng.integers(1, 700, batch), hq, hkv, splits, psize=16)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seed", range(8))
+def test_fused_qkv_decode_attention_random_shapes(device, seed):
+    """The same bitwise check over a seeded sweep: batch 1-40, GQA 1-8, 1-8 KV heads, 1-10 QKV splits, pages of
+    16 or 32 tokens, contexts 1-600 with the new token on block and page edges (first token of a sequence, last of
+    a tile or block, first of the next) so that it lands in every wavefront position, past-the-end tiles included."""
+    rng = np.random.default_rng(2000 + seed)
+    batch = int(rng.integers(1, 41))
+    g, hkv = int(rng.integers(1, 9)), int(rng.choice([1, 2, 4, 8]))
+    edges = np.array([1, 2, 16, 17, 31, 32, 33, 64, 65, 256, 257])
+    lens = np.where(rng.random(batch) < 0.4, rng.choice(edges, batch), rng.integers(1, 601, batch))
+    _fused_equals_two_kernels(device, rng, lens, g * hkv, hkv, int(rng.integers(1, 11)),
+                              psize=int(rng.choice([16, 32])))
+
+
+def _fused_equals_two_kernels(device, rng, lens, hq, hkv, splits, psize):
     from cacheir_amd import kernels
 
-    rng = np.random.default_rng(batch * 100 + hq)
-    d, psize = 128, 16
-    lens = rng.integers(1, 700, batch).astype(np.int32)          # after the append
+    d = 128
+    batch = len(lens)
+    lens = np.asarray(lens).astype(np.int32)                        # after the append
     positions = (lens - 1).astype(np.int32)
     pages = [-(-int(n) // psize) for n in lens]
     max_pages = max(pages) + 1

@@ -1232,13 +1232,15 @@ bool gemv_head_fits(int fmt, int m, int k) { return !is_row_fmt(fmt) && gemv_fit
 #define CIR_XS_KG 1
 #endif
 
-// k-groups per workgroup: a divisor of the split's quad count.  Two where a split
-// has 32 quads or more, at any m (measured: the unsplit gate|up + SwiGLU at k = 4096
-// gains ~4% at m = 32 and ~10% at m = 1; splits of 4-14 quads lose with half as many
-// per group).  Every epilogue of this kernel (partials, SwiGLU, argmax) picks the
-// same value for the same m and k, so their sums run in the same order.
-int xs_kgroups(int m, int quads) {
-  int kg = quads >= 32 ? 2 : (m > 16 ? CIR_XS_KG : 1);
+// k-groups per workgroup: a divisor of the split's quad count.  Two where a split has
+// 32 quads or more and the launch has at most one workgroup per CU, at any m
+// (measured: the unsplit gate|up + SwiGLU at k = 4096, 224 workgroups, gains ~4% at
+// m = 32 and ~10% at m = 1; the lm_head's 1002 workgroups lose 15%, and splits of
+// 4-14 quads lose with half as many per group).  Every epilogue of this kernel
+// (partials, SwiGLU, argmax) picks the same value for the same m, n and k, so their
+// sums run in the same order.
+int xs_kgroups(int m, int quads, long workgroups) {
+  int kg = (quads >= 32 && workgroups <= kCUs) ? 2 : (m > 16 ? CIR_XS_KG : 1);
   while (kg > 1 && quads % kg) kg /= 2;
   return kg;
 }
@@ -1252,7 +1254,7 @@ void launch_qgemm_swiglu(const f16* x, int ldx, const uint8_t* wq, const uint16_
     qgemm_xs_kernel<FMT, 2, MT, CIR_XS_DW_SWIGLU, 1, TO, KG>
         <<<grid, 256 * KG, 0, s>>>(x, ldx, wq, wd, nullptr, M, N, K, K / 128, act);
   };
-  const int kg = xs_kgroups(M, K / 128);
+  const int kg = xs_kgroups(M, K / 128, (long)grid.x * grid.y * grid.z);
   if constexpr (CIR_XS_KG >= 4) {
     if (kg == 4) return go.template operator()<4>();
   }
@@ -1321,7 +1323,7 @@ void launch_qgemm_argmax(const f16* x, int ldx, const uint8_t* wq, const uint16_
     qgemm_xs_kernel<FMT, NT, MT, (MT == 1 ? 4 : CIR_XS_DW), 2, float, KG>
         <<<grid, 256 * KG, 0, s>>>(x, ldx, wq, wd, cand_v, M, N, K, quads, reinterpret_cast<float*>(cand_i));
   };
-  const int kg = xs_kgroups(M, quads);
+  const int kg = xs_kgroups(M, quads, (long)grid.x * grid.y * grid.z);
   if constexpr (CIR_XS_KG >= 4) {
     if (kg == 4) return go.template operator()<4>(), argmax_cand_kernel<<<M, 256, 0, s>>>(cand_v, cand_i, (int)grid.x * 4, M, ids);
   }
@@ -1339,7 +1341,7 @@ void launch_qgemm_xs(const f16* x, int ldx, const uint8_t* wq, const uint16_t* w
   auto go = [&]<int KG>() {
     qgemm_xs_kernel<FMT, NT, MT, DW, 0, float, KG><<<grid, 256 * KG, 0, s>>>(x, ldx, wq, wd, part, M, N, K, quads);
   };
-  const int kg = xs_kgroups(M, quads);
+  const int kg = xs_kgroups(M, quads, (long)grid.x * grid.y * grid.z);
   if constexpr (CIR_XS_KG >= 4) {
     if (kg == 4) return go.template operator()<4>();
   }

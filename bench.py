@@ -372,8 +372,9 @@ def main() -> int:
     art = compile_config(cfg, quant="q4_0", modes=("decode",))
     pages_per_seq = -(-ctx // P)
     t0 = time.time()
+    # one lane of pages_per_seq slots for each session (the base runtime's own included), so no lane runs dry
     base = HipRuntime(art, source=SyntheticQuant(GGML_Q4_0, dev, seed=0),
-                      kv_capacity_pages=B * pages_per_seq + 8)
+                      kv_capacity_pages=(B + 1) * pages_per_seq)
     sessions = [base.fork() for _ in range(B)]
     for s in sessions:
         s.kv_cache.ensure_capacity(ctx)

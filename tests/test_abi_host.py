@@ -148,10 +148,54 @@ def test_kv_pages_refcount_alias_and_copy_on_write():
     dst2.ensure_capacity(5)
     assert dst2.slots[0] == src.slots[0] and len(dst2.slots) == 2 and dst2.slots[1] not in src.slots
     # releasing every user frees the pages
-    before = len(a._free)
+    before = a.free_pages
     for c in (dst, dst2, src):
         c.clear()
-    assert a.stats()["resident_pages"] == 0 and len(a._free) == before + 4
+    assert a.stats()["resident_pages"] == 0 and a.free_pages == before + 4
+
+
+def test_kv_lanes_keep_a_batch_page_major():
+    """Sessions of equal length hold page i side by side (stripe i), whether they allocate one after another or a
+    page at a time; a dry lane borrows from the fullest one before the pool grows; released slots are reused lowest
+    stripe first."""
+    from cacheir_amd.kv import HipKVPageAllocator, HipPagedKVCache
+
+    L, B, pages = 5, 4, 6
+    a = HipKVPageAllocator(num_layers=1, kv_heads=1, head_dim=4, page_size=4, dtype=torch.float32, device="cpu",
+                           capacity_pages=L * pages, lanes=L)
+    assert a.capacity == L * pages and a.free_pages == L * pages
+    one_by_one = [HipPagedKVCache(a) for _ in range(B)]
+    for c in one_by_one:
+        c.ensure_capacity(4 * pages)
+    lanes = [c.lane for c in one_by_one]
+    assert lanes == list(range(B))
+    for c in one_by_one:
+        assert c.slots == [i * L + c.lane for i in range(pages)]
+    for c in one_by_one:
+        c.clear()
+    assert a.free_pages == L * pages
+    # a page at a time (decode appends): the same placement
+    stepped = [HipPagedKVCache(a, lane=b) for b in range(B)]
+    for t in range(1, 4 * pages + 1):
+        for c in stepped:
+            c.ensure_capacity(t)
+    for c in stepped:
+        assert c.slots == [i * L + c.lane for i in range(pages)]
+    # lane 4 holds 6 free slots; lanes 0-3 none: a session in lane 0 borrows lane 4's before the pool grows
+    extra = HipPagedKVCache(a, lane=0)
+    extra.ensure_capacity(4 * 3)
+    assert extra.slots == [4, 9, 14] and a.pool_grows == 1
+    extra.ensure_capacity(4 * 6)
+    assert a.pool_grows == 1 and a.free_pages == 0
+    extra.ensure_capacity(4 * 7)  # nothing free anywhere: the pool doubles in whole stripes
+    assert a.pool_grows == 2 and a.capacity == 2 * L * pages and a.capacity % L == 0
+    assert extra.slots[-1] == L * pages  # lane 0's first new stripe
+    stepped[2].clear()
+    again = HipPagedKVCache(a, lane=2)
+    again.ensure_capacity(4 * 2)
+    assert again.slots == [2, 2 + L]
+    used = [s for c in stepped + [extra, again] for s in c.slots]
+    assert len(used) == len(set(used)) and all(a.refcount(s) == 1 for s in used)
 
 
 def test_prefix_cache_holds_and_releases_pages():

@@ -23,20 +23,6 @@ namespace {
 
 bool valid_dt(int dt) { return dt == CIR_F32 || dt == CIR_F16; }
 
-// ---------------------------------------------------------------- embedding --
-template <typename TT, typename TO>
-__global__ void embedding_kernel(const int64_t* __restrict__ ids, const TT* __restrict__ table, TO* __restrict__ out,
-                                 int hidden, int vocab) {
-  const int r = blockIdx.x;
-  int64_t id = ids[r];
-  // Out-of-range ids are clamped, so no id reads outside the table; the runtime
-  // rejects them on the host before they get here.
-  id = id < 0 ? 0 : (id >= vocab ? vocab - 1 : id);
-  const TT* src = table + (size_t)id * hidden;
-  TO* dst = out + (size_t)r * hidden;
-  for (int i = threadIdx.x; i < hidden; i += blockDim.x) dst[i] = from_f32<TO>(to_f32(src[i]));
-}
-
 // ---------------------------------------------------------------- rmsnorm ----
 constexpr int kRowThreads = 1024;
 constexpr int kRowVals = 8;  // rows up to 8192 stay in registers
@@ -109,6 +95,43 @@ __device__ __forceinline__ float4 load4(const f16* p) {
 __device__ __forceinline__ void store4(float* p, float4 v) { *reinterpret_cast<float4*>(p) = v; }
 __device__ __forceinline__ void store4(f16* p, float4 v) {
   *reinterpret_cast<f16x4*>(p) = f16x4{(f16)v.x, (f16)v.y, (f16)v.z, (f16)v.w};
+}
+
+// ---------------------------------------------------------------- embedding --
+// One workgroup per row.  VEC: hidden % 4 == 0 and 16-byte aligned rows, 4 values per
+// access with kEmbUnroll accesses of a thread issued before its first store (a row of
+// 4096 is one round trip); otherwise one value at a time.
+constexpr int kEmbThreads = 256;
+constexpr int kEmbUnroll = 4;
+template <typename TT, typename TO, bool VEC>
+__global__ __launch_bounds__(kEmbThreads) void embedding_kernel(const int64_t* __restrict__ ids,
+                                                                const TT* __restrict__ table, TO* __restrict__ out,
+                                                                int hidden, int vocab) {
+  const int r = blockIdx.x;
+  int64_t id = ids[r];
+  // Out-of-range ids are clamped, so no id reads outside the table; the runtime
+  // rejects them on the host before they get here.
+  id = id < 0 ? 0 : (id >= vocab ? vocab - 1 : id);
+  const TT* src = table + (size_t)id * hidden;
+  TO* dst = out + (size_t)r * hidden;
+  if constexpr (VEC) {
+    const int n4 = hidden / 4;
+    for (int base = threadIdx.x; base < n4; base += kEmbThreads * kEmbUnroll) {
+      float4 v[kEmbUnroll];
+#pragma unroll
+      for (int u = 0; u < kEmbUnroll; ++u) {
+        const int i = base + u * kEmbThreads;
+        if (i < n4) v[u] = load4(src + 4 * i);
+      }
+#pragma unroll
+      for (int u = 0; u < kEmbUnroll; ++u) {
+        const int i = base + u * kEmbThreads;
+        if (i < n4) store4(dst + 4 * i, v[u]);
+      }
+    }
+  } else {
+    for (int i = threadIdx.x; i < hidden; i += kEmbThreads) dst[i] = from_f32<TO>(to_f32(src[i]));
+  }
 }
 
 // Residual epilogue + RMSNorm of the result, one workgroup per row, 4 columns per
@@ -346,15 +369,17 @@ extern "C" int cir_embedding(const int64_t* ids, const void* table, int tdt, voi
   if (rows == 0 || hidden == 0) return 0;
   CIR_CHECK_ARG(ids && table && out, "embedding: null pointer");
   hipStream_t s = as_stream(stream);
-  const int bs = 256;
-  if (tdt == CIR_F32 && odt == CIR_F32)
-    embedding_kernel<float, float><<<rows, bs, 0, s>>>(ids, (const float*)table, (float*)out, hidden, vocab);
-  else if (tdt == CIR_F16 && odt == CIR_F32)
-    embedding_kernel<f16, float><<<rows, bs, 0, s>>>(ids, (const f16*)table, (float*)out, hidden, vocab);
-  else if (tdt == CIR_F16 && odt == CIR_F16)
-    embedding_kernel<f16, f16><<<rows, bs, 0, s>>>(ids, (const f16*)table, (f16*)out, hidden, vocab);
-  else
-    embedding_kernel<float, f16><<<rows, bs, 0, s>>>(ids, (const float*)table, (f16*)out, hidden, vocab);
+  // 4-value accesses need every row 8- (fp16) or 16-byte (fp32) aligned: base pointers on 16 bytes, hidden % 4 == 0.
+  const bool vec = hidden % 4 == 0 && reinterpret_cast<uintptr_t>(table) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(out) % 16 == 0;
+  auto go = [&]<typename TT, typename TO>() {
+    if (vec) embedding_kernel<TT, TO, true><<<rows, kEmbThreads, 0, s>>>(ids, (const TT*)table, (TO*)out, hidden, vocab);
+    else embedding_kernel<TT, TO, false><<<rows, kEmbThreads, 0, s>>>(ids, (const TT*)table, (TO*)out, hidden, vocab);
+  };
+  if (tdt == CIR_F32 && odt == CIR_F32) go.template operator()<float, float>();
+  else if (tdt == CIR_F16 && odt == CIR_F32) go.template operator()<f16, float>();
+  else if (tdt == CIR_F16 && odt == CIR_F16) go.template operator()<f16, f16>();
+  else go.template operator()<float, f16>();
   return launch_status();
 }
 

@@ -662,6 +662,17 @@ def test_row_kernels(device):
     ids = np.array([3, 0, 49, 7], dtype=np.int64)
     emb = kernels.embedding(to_dev(ids, device), to_dev(table, device), torch.float32).cpu().numpy()
     assert np.array_equal(emb, table[ids].astype(np.float32))
+    # 4-value accesses (hidden % 4 == 0, rows past one unrolled pass) and the one-value path (hidden 4099), every
+    # table/output dtype pair, bit for bit
+    for hidden in (4096, 5120, 4099):
+        tab = rng.standard_normal((64, hidden)).astype(np.float32)
+        ids = rng.integers(0, 64, 9).astype(np.int64)
+        for tdt in (torch.float16, torch.float32):
+            t = to_dev(tab, device).to(tdt)
+            ref = t.cpu()[torch.from_numpy(ids)]
+            for odt in (torch.float16, torch.float32):
+                got = kernels.embedding(to_dev(ids, device), t, odt).cpu()
+                assert torch.equal(got, ref.to(odt)), (hidden, tdt, odt)
     logits = rng.standard_normal((3, 1000)).astype(np.float32)
     logits[1, 10] = logits[1, 20] = 50.0  # tie -> first index
     got = kernels.argmax(to_dev(logits, device)).cpu().numpy()

@@ -1351,6 +1351,13 @@ void launch_qgemm_xs(const f16* x, int ldx, const uint8_t* wq, const uint16_t* w
 
 // Large m: activation rows per workgroup (16 * MT).
 constexpr int xl_mt(int m) { return m <= 64 ? 4 : 8; }
+// The SwiGLU launch (one split, so the column groups alone set the workgroup count)
+// keeps 64 rows per workgroup up to m = 128: at the Qwen2-7B gate|up (n 37888, 296
+// column groups) 128 rows per workgroup leave 296 workgroups, a second round on 40 CUs,
+// while two 64-row blocks give 592 smaller ones at 3 wavefronts per SIMD (158 VGPRs
+// against 202): 83.2-86.0 us against 90.3-90.9 (Q8_0, m = 128, same box, alternated).
+// The partials launch keeps xl_mt (QKV, n 4608: 19.3 us at 64 rows against 16.4).
+constexpr int xl_mt_swiglu(int m) { return m <= 128 ? 4 : 8; }
 
 // m > 32 takes the large-m kernel when n spans at least 36 groups of 128 columns.
 // Measured at the Qwen2-7B shapes (Q8_0, m = 64 / 128) against the m <= 32 kernel
@@ -1567,7 +1574,7 @@ extern "C" int cir_qgemm_swiglu(const void* x, int ldx, const void* w_tiled, int
         if (odt == CIR_F16) launch_qgemm_xl<FMT, MT, 1, f16>(xh, ldx, q, d, nullptr, m, n, k, 1, s, static_cast<f16*>(out));
         else launch_qgemm_xl<FMT, MT, 1, float>(xh, ldx, q, d, nullptr, m, n, k, 1, s, static_cast<float*>(out));
       };
-      if (xl_mt(m) == 4) xl.template operator()<4>();
+      if (xl_mt_swiglu(m) == 4) xl.template operator()<4>();
       else xl.template operator()<8>();
       return;
     }
@@ -1651,7 +1658,8 @@ extern "C" const char* cir_qgemm_plan(int op, int fmt, int m, int n, int k, int 
       if (!use_xl(m, n)) return "qgemm_xs_kernel<NT=2,MT=2>";
       return m <= 64 ? "qgemm_xl_kernel<MT=4>" : "qgemm_xl_kernel<MT=8>";
     case CIR_GEMM_SWIGLU:
-      if (use_xl(m, n)) return xl_mt(m) == 4 ? "qgemm_xl_kernel<MT=4,EPI=swiglu>" : "qgemm_xl_kernel<MT=8,EPI=swiglu>";
+      if (use_xl(m, n))
+        return xl_mt_swiglu(m) == 4 ? "qgemm_xl_kernel<MT=4,EPI=swiglu>" : "qgemm_xl_kernel<MT=8,EPI=swiglu>";
       return m <= 16 ? "qgemm_xs_kernel<NT=2,MT=1,EPI=swiglu>" : "qgemm_xs_kernel<NT=2,MT=2,EPI=swiglu>";
     case CIR_GEMM_ARGMAX:
       if (gemv_head_fits(fmt, m, k)) return "qgemv_kernel<EPI=argmax>+argmax_cand_kernel";

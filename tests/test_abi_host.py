@@ -198,6 +198,59 @@ def test_kv_lanes_keep_a_batch_page_major():
     assert len(used) == len(set(used)) and all(a.refcount(s) == 1 for s in used)
 
 
+def test_kv_allocator_random_sequences_keep_invariants():
+    """Random mixes of sessions growing, copying on write, aliasing prefixes and releasing pages, over several lane
+    counts: no slot is held twice, the free count and the per-lane free heaps always account for every slot, refcounts
+    equal the number of page tables (and cache holds) using a slot, and capacity stays a whole number of stripes."""
+    import numpy as np
+
+    from cacheir_amd.kv import HipKVPageAllocator, HipPagedKVCache
+
+    for lanes, seed in ((1, 0), (3, 1), (5, 2), (33, 3)):
+        rng = np.random.default_rng(seed)
+        a = HipKVPageAllocator(num_layers=1, kv_heads=1, head_dim=4, page_size=4, dtype=torch.float32, device="cpu",
+                               capacity_pages=7, lanes=lanes)
+        caches: list[HipPagedKVCache] = []
+        held: list[list[int]] = []  # extra references (a prefix cache would hold)
+        for _ in range(400):
+            op = rng.integers(0, 6)
+            if op == 0 or not caches:
+                caches.append(HipPagedKVCache(a))
+            c = caches[int(rng.integers(0, len(caches)))]
+            if op in (0, 1):
+                c.ensure_capacity(c.tokens + int(rng.integers(1, 20)))
+                c.tokens = len(c.slots) * 4 - int(rng.integers(0, 4))
+            elif op == 2 and c.tokens:
+                src = caches[int(rng.integers(0, len(caches)))]
+                if src is not c and src.tokens:
+                    n = int(rng.integers(1, src.tokens + 1))
+                    c.alias_prefix(list(src.slots), n)
+            elif op == 3 and c.tokens:
+                a.share(list(c.slots))
+                held.append(list(c.slots))
+            elif op == 4 and held:
+                a.release(held.pop(int(rng.integers(0, len(held)))))
+            elif op == 5:
+                c.clear()
+            # invariants
+            uses: dict[int, int] = {}
+            for cc in caches:
+                for sl in cc.slots:
+                    uses[sl] = uses.get(sl, 0) + 1
+            for h in held:
+                for sl in h:
+                    uses[sl] = uses.get(sl, 0) + 1
+            assert all(a.refcount(sl) == n for sl, n in uses.items())
+            assert a.stats()["resident_pages"] == len(uses)
+            free = [sl for heap in a._lane_free for sl in heap]
+            assert len(free) == len(set(free)) == a.free_pages
+            assert not set(free) & set(uses)
+            assert len(free) + len(uses) == a.capacity and a.capacity % lanes == 0
+            for ln, heap in enumerate(a._lane_free):  # each lane's free slots: its own, in min-heap order
+                assert all(sl % lanes == ln for sl in heap)
+                assert all(heap[(i - 1) // 2] <= heap[i] for i in range(1, len(heap)))
+
+
 def test_prefix_cache_holds_and_releases_pages():
     from cacheir_amd.kv import HipPagedKVCache
     from cacheir_amd.runtime import PrefixCache, PrefixPages

@@ -473,14 +473,16 @@ def test_o_projection_from_attention_parts(device, fmt, lens, hq, hkv, want_s):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
-@pytest.mark.parametrize("m,k", [(1, 512), (8, 512), (32, 512), (48, 512), (128, 640), (1, 4096), (3, 4096),
-                                 (8, 4096), (16, 4096), (32, 4096)])
+@pytest.mark.parametrize("m,k", [(1, 512), (8, 512), (32, 512), (48, 512), (100, 640), (128, 640), (200, 640),
+                                 (1, 4096), (3, 4096), (8, 4096), (16, 4096), (32, 4096)])
 def test_qgemm_swiglu_matches_gemm_then_epilogue(device, fmt, m, k):
     """cir_qgemm_swiglu over interleaved gate/up tiles == cir_qgemm (splits 1) + cir_epilogue_swiglu, bitwise,
     and within the fp16 bound of the fp64 oracle. At m <= 8 the reference side runs the GEMV (k = 4096 stages
     all of an 8-row activation in 64 KiB of LDS): with 32 quads or more the fused kernel sums two k-groups (even
     and odd quads) and then adds them, the GEMV sums the quads in order, so there the outputs agree to one fp16
-    ulp (the fp32 sums differ in rounding only); with fewer quads, bit for bit."""
+    ulp (the fp32 sums differ in rounding only); with fewer quads, bit for bit.  m = 100 and 128 run the large-m
+    SwiGLU in 64-row blocks against 128-row blocks for the partials (a partly filled last block at 100), m = 200 in
+    128-row blocks."""
     from cacheir_amd import kernels
 
     rng = np.random.default_rng(11 + m + k)

@@ -281,6 +281,38 @@ def ragged_attention_case(config: int, dev, iters: int) -> dict:
     return res
 
 
+def prefill_case(base, cfg, tokens: int, dev) -> dict:
+    """Prefill measured (the step before decode): one prompt of ``tokens`` ids through ``HipRuntime.run`` on the
+    base session (causal paged attention writing the pool, projections on the large-m MFMA GEMM, logits for every
+    position), best of 3 timed runs after a warm-up, host launches included.  FLOPs: 2 per weight per token for the
+    linear layers and the lm_head, plus q.k and p.v over the causal context."""
+    import torch
+
+    ids = np.random.default_rng(3).integers(0, cfg.vocab_size, size=(1, tokens))
+    out = base.run(ids, mode="prefill")
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        out = base.run(ids, mode="prefill")
+        torch.cuda.synchronize()
+        times.append(time.perf_counter() - t0)
+    if not bool(torch.isfinite(out).all()):
+        raise RuntimeError("prefill: non-finite logits")
+    del out
+    ms = min(times) * 1e3
+    h, f, d = cfg.hidden_size, cfg.intermediate_size, cfg.head_dim
+    per_layer = h * (cfg.num_attention_heads + 2 * cfg.num_key_value_heads) * d + cfg.num_attention_heads * d * h \
+        + 3 * h * f
+    params = cfg.num_layers * per_layer + cfg.vocab_size * h
+    attn = cfg.num_layers * 4 * cfg.num_attention_heads * d * tokens * (tokens + 1) // 2
+    tflops = (2 * tokens * params + attn) / (ms * 1e-3) / 1e12
+    torch.cuda.empty_cache()
+    return {"tokens": tokens, "batch": 1, "ms": round(ms, 3), "tokens_per_s": round(tokens / ms * 1e3, 1),
+            "tflops": round(tflops, 1), "frac_mfma": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
+            "note": "HipRuntime.run(mode='prefill') wall time, host launches included; logits for every position"}
+
+
 def gemm_rooflines(base, cfg, B, dev, args) -> dict:
     """The projection rooflines: the fused gate|up GEMM + SwiGLU at m = batch, BASELINE config 3 (m = 1, 8, 32)
     and the batched GEMM of config 5 (Q8_0 gate|up at m = 128), each timed live as HIP-graph replays."""
@@ -369,7 +401,7 @@ def main() -> int:
         del src, dst
     cfg = llama3_8b(args.layers)
     B, ctx, P = args.batch, args.ctx, 16
-    art = compile_config(cfg, quant="q4_0", modes=("decode",))
+    art = compile_config(cfg, quant="q4_0", modes=("prefill", "decode"))
     pages_per_seq = -(-ctx // P)
     t0 = time.time()
     # one lane of pages_per_seq slots for each session (the base runtime's own included), so no lane runs dry
@@ -478,6 +510,9 @@ def main() -> int:
         host_steps[name] = r
         log(f"runtime API {name}: decode_greedy {r['decode_greedy_ms']:.3f} ms, run_decode_batch "
             f"{r['run_decode_batch_ms']:.3f} ms (graph step {graph_ms:.3f} ms)")
+    prefill = prefill_case(base, cfg, ctx, dev)
+    log(f"prefill {prefill['tokens']} tokens {prefill['ms']:.2f} ms -> {prefill['tokens_per_s']:.0f} tok/s, "
+        f"{prefill['tflops']:.0f} TFLOP/s ({prefill['frac_mfma']:.1%} of fp16 MFMA)")
     gemm_plans = base.cache_stats()["gemm_plans"]
 
     traffic = measured_traffic(TRAFFIC_FILE)
@@ -534,6 +569,7 @@ def main() -> int:
         "decode_batch1": {"ms_per_step": round(ms_b1, 4), "tokens_per_s": round(1000.0 / ms_b1, 2),
                           "hbm_floor_ms": round((weight_bytes + kv_b1) / HBM_PEAK_GBS / 1e6, 4),
                           "note": "same model and context, one sequence; projections on the dequant GEMV"},
+        "prefill": prefill,
         "runtime_api_steps": {"note": "wall ms per step through HipRuntime.decode_greedy / run_decode_batch (+ "
                                       "synchronize), host work included, graph replay per step",
                               **host_steps},

@@ -24,6 +24,8 @@
 //     ds_bpermute shuffles, in fp16 with two heads per dword (l sums the same
 //     rounded values); the four token groups are summed once at the end;
 //   * the 8 wavefronts merge (max, sum, O) through LDS with log-sum-exp weights.
+// Prefill (q_len > 1) on fp16 pools runs attn_prefill_f16_d128 instead: 128 query
+// vectors of a sequence per workgroup over its blocks, both products on MFMA.
 // fp32 pools and other head sizes (tiny-model parity path) use a plain VALU kernel
 // over 128-token chunks that always writes partials, merged by the same kernel.
 //
@@ -546,6 +548,188 @@ __global__ __launch_bounds__(64 * kWaves) void attn_f16_d128(
 }
 
 // ----------------------------------------------------------------------------
+// Prefill (q_len > 1), fp16 pools, head_dim 128, G <= 8.  The query vectors of one
+// sequence and KV head (vector v = t * G + g over its q_len new tokens) form 16-vector
+// tiles, one per wavefront, kPfWaves per workgroup.  A workgroup walks the 32-token
+// K/V blocks its last token sees, kPfGroup blocks at a time: every K and V load of a
+// group is issued at once, while the previous group is being multiplied, and lands in
+// LDS (V transposed) in the other of two buffers.  Each block is read once per 128 query
+// vectors instead of once per query row.  Both products run on MFMA 16x16x32 f16:
+//   * S^T = K Q^T: A = 16 token rows of K (lane t + 16g holds K[t][32s + 8g ..]), B =
+//     Q^T (lane q + 16g holds Q[q][32s + 8g ..]); lane q + 16g ends with S[q][4g + r]
+//     of each 16-token tile;
+//   * O = P V: the A operand is P as the lanes already hold it -- lane q + 16g takes
+//     P[q][4g .. 4g+3] of tile 0 and P[q][16 + 4g .. +3] of tile 1 as its 8 k values --
+//     and V's B operand takes the same token order (lane d + 16g: V^T[d] at tokens 4g ..
+//     and 16 + 4g ..), so no lane exchange is needed.
+// Causal mask per query vector (keys at positions <= its token's), softmax as in the
+// decode kernel (base 2, p rounded to fp16, l summing the rounded p).  A wavefront skips
+// the blocks past its last token.  The tiles of a sequence are dispatched last first, so
+// the longest contexts start first.
+constexpr int kPfWaves = 8;
+constexpr int kPfGroup = 4;    // blocks per LDS buffer (two buffers: 140 KiB)
+constexpr int kPfKRow = 136;   // K row stride in LDS (halves): 256 B + 16, a tile's rows on distinct banks
+constexpr int kPfVRow = 36;    // V^T row stride (halves): 64 B + 8
+
+__global__ __launch_bounds__(64 * kPfWaves) void attn_prefill_f16_d128(
+    const f16* __restrict__ q, const f16* __restrict__ kp, const f16* __restrict__ vp,
+    const int32_t* __restrict__ pt, const int32_t* __restrict__ lens, f16* __restrict__ out, int q_len, int Hq,
+    int Hkv, int P, int max_pages, float scale_log2) {
+  constexpr int D = 128;
+  static_assert(kBlock == 32 && 64 * kPfWaves == kBlock * (D / 8), "one 16-byte K and V chunk per thread");
+  __shared__ __align__(16) f16 sk[2][kPfGroup][kBlock * kPfKRow];
+  __shared__ __align__(16) f16 sv[2][kPfGroup][D * kPfVRow];
+  const int tile = gridDim.x - 1 - blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  const int G = Hq / Hkv;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int li = lane & 15, lg = lane >> 4;
+  const int nvec = q_len * G;
+  const int max_ctx = max_pages * P;
+  const int L = lens[b];
+  const int Lc = min(L, max_ctx);  // keys the page table can address
+  const int past = L - q_len;      // context before the new tokens
+  const int32_t* ptrow = pt + (size_t)b * max_pages;
+  // Last key position query vector v sees (negative: none, its output is zero).
+  auto pos_of = [&](int v) __attribute__((always_inline)) { return min(past + v / G, Lc - 1); };
+  const int tv0 = tile * 16 * kPfWaves;                     // the workgroup's first vector
+  const int tv1 = min(nvec, tv0 + 16 * kPfWaves) - 1;       // and its last
+  const int nblk = pos_of(tv1) >= 0 ? pos_of(tv1) / kBlock + 1 : 0;  // blocks the last token sees
+  const int v0 = tv0 + 16 * wave;                           // this wavefront's first vector
+  const int wlast = min(nvec - 1, v0 + 15);
+  const int wblk = (v0 < nvec && pos_of(wlast) >= 0) ? pos_of(wlast) / kBlock + 1 : 0;  // uniform
+
+  // Thread t loads 16 bytes of K and of V per block: token t / 16, dims 8 * (t % 16).
+  const int lt = threadIdx.x >> 4, lc = threadIdx.x & 15;
+  f16x8 kr[kPfGroup], vr[kPfGroup];
+  auto load_group = [&](int g0, int nb) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < kPfGroup; ++i) {
+      if (i < nb) {
+        const int tok = min((g0 + i) * kBlock + lt, Lc - 1);  // past the context: masked, a valid page
+        const int page = ptrow[tok / P];
+        const size_t at = (((size_t)page * Hkv + kvh) * P + tok % P) * D + 8 * lc;
+        kr[i] = *reinterpret_cast<const f16x8*>(kp + at);
+        vr[i] = *reinterpret_cast<const f16x8*>(vp + at);
+      }
+    }
+  };
+  auto stash_group = [&](int buf, int nb) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < kPfGroup; ++i) {
+      if (i < nb) {
+        *reinterpret_cast<f16x8*>(&sk[buf][i][lt * kPfKRow + 8 * lc]) = kr[i];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sv[buf][i][(8 * lc + e) * kPfVRow + lt] = vr[i][e];
+      }
+    }
+  };
+  if (nblk > 0) load_group(0, min(kPfGroup, nblk));
+
+  // Q^T as the B operand (zero past the last vector), and each lane's query position.
+  f16x8 qb[4];
+  const int vq = v0 + li;
+  const bool live = vq < nvec;
+  const int qpos = pos_of(live ? vq : nvec - 1);
+  {
+    const int vv = live ? vq : 0;
+    const int t = vv / G, g = vv - t * G;
+    const f16* qrow = q + (((size_t)b * q_len + t) * Hq + (size_t)kvh * G + g) * D + 8 * lg;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const f16x8 x = *reinterpret_cast<const f16x8*>(qrow + 32 * s);
+      qb[s] = live ? x : f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+    }
+  }
+  if (nblk > 0) stash_group(0, min(kPfGroup, nblk));
+  __syncthreads();
+
+  float m = -INFINITY, l = 0.f;  // query li: running max (every lane of the query), this lane's share of the sum
+  f32x4 acc[D / 16];             // O[query 4 lg + r][16 dt + li]
+#pragma unroll
+  for (int dt = 0; dt < D / 16; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  auto block = [&](int buf, int i, int blk) __attribute__((always_inline)) {
+    f32x4 c[kTiles];
+#pragma unroll
+    for (int j = 0; j < kTiles; ++j) {
+      c[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const f16x8 a = *reinterpret_cast<const f16x8*>(&sk[buf][i][(16 * j + li) * kPfKRow + 32 * s + 8 * lg]);
+        c[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qb[s], c[j], 0, 0, 0);
+      }
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < kTiles; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int key = blk * kBlock + 16 * j + 4 * lg + r;
+        c[j][r] = key <= qpos ? c[j][r] * scale_log2 : -INFINITY;
+        mx = fmaxf(mx, c[j][r]);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    // Block 0 comes first and key 0 is visible to every query with a position, so m is finite from then on and
+    // a fully masked later block leaves mn = m, alpha = 1 and p = 0.  A query with no key at all keeps m = -inf:
+    // alpha 1 and p 0 (not the NaN of -inf - -inf), l stays 0 and its output 0.
+    const float mn = fmaxf(m, mx);
+    const bool none = mn == -INFINITY;
+    const float alpha = none ? 1.f : exp2f(m - mn);
+    f16x8 pa;
+    float ps = 0.f;
+#pragma unroll
+    for (int j = 0; j < kTiles; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const f16 p = static_cast<f16>(none ? 0.f : exp2f(c[j][r] - mn));
+        pa[4 * j + r] = p;
+        ps += static_cast<float>(p);
+      }
+    l = l * alpha + ps;
+    m = mn;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float ar = __shfl(alpha, 4 * lg + r, 64);
+#pragma unroll
+      for (int dt = 0; dt < D / 16; ++dt) acc[dt][r] *= ar;
+    }
+#pragma unroll
+    for (int dt = 0; dt < D / 16; ++dt) {
+      const f16* vrow = &sv[buf][i][(16 * dt + li) * kPfVRow];
+      const f16x4 lo = *reinterpret_cast<const f16x4*>(vrow + 4 * lg);
+      const f16x4 hi = *reinterpret_cast<const f16x4*>(vrow + 16 + 4 * lg);
+      const f16x8 vb = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, vb, acc[dt], 0, 0, 0);
+    }
+  };
+  int buf = 0;
+  for (int g0 = 0; g0 < nblk; g0 += kPfGroup, buf ^= 1) {  // uniform
+    const int nb = min(kPfGroup, nblk - g0);
+    const int g1 = g0 + kPfGroup, nb1 = min(kPfGroup, nblk - g1);
+    if (nb1 > 0) load_group(g1, nb1);  // in flight during this group's math
+    for (int i = 0; i < nb; ++i)
+      if (g0 + i < wblk) block(buf, i, g0 + i);
+    if (nb1 > 0) stash_group(buf ^ 1, nb1);
+    __syncthreads();
+  }
+  l += __shfl_xor(l, 16, 64);
+  l += __shfl_xor(l, 32, 64);
+
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int v = v0 + 4 * lg + r;
+    const float lr = __shfl(l, 4 * lg + r, 64);
+    if (v < nvec) {
+      const int t = v / G, g = v - t * G;
+      f16* po = out + (((size_t)b * q_len + t) * Hq + (size_t)kvh * G + g) * D + li;
+      const float inv = lr > 0.f ? 1.f / lr : 0.f;
+#pragma unroll
+      for (int dt = 0; dt < D / 16; ++dt) po[16 * dt] = static_cast<f16>(acc[dt][r] * inv);
+    }
+  }
+}
+
+// ----------------------------------------------------------------------------
 // Generic VALU kernel (fp32 or fp16 pools, any page size, head_dim <= 256):
 // one wavefront per (128-token chunk, KV head, row); always writes partials.
 template <typename T>
@@ -753,6 +937,13 @@ int launch_attention(const void* q, const void* k_pool, const void* v_pool, cons
   float* part_o = static_cast<float*>(workspace);
   float* part_ml = part_o + (size_t)rows * Hq * S * D;
   dim3 grid(S, Hkv, rows);
+  if (mfma && q_len > 1) {  // prefill: query tiles of 128 vectors over each sequence's blocks, no partials
+    const int tiles = (q_len * G + 16 * kPfWaves - 1) / (16 * kPfWaves);
+    attn_prefill_f16_d128<<<dim3(tiles, Hkv, batch), 64 * kPfWaves, 0, s>>>(
+        static_cast<const f16*>(q), static_cast<const f16*>(k_pool), static_cast<const f16*>(v_pool), page_table,
+        seq_lens, static_cast<f16*>(out), q_len, Hq, Hkv, P, max_pages, scale_log2);
+    return launch_status();
+  }
   if (mfma) {
     // Longest rows first when the workgroups outnumber the CUs (they then run in rounds).
     const int sort_rows = q_len == 1 && rows <= 64 * kWaves && (long)S * Hkv * rows > device_cus();

@@ -174,6 +174,34 @@ def test_prefill_attention_causal(device, dtype):
             close16(out[b * q_len:(b + 1) * q_len], ref)
 
 
+@pytest.mark.parametrize("seed", range(8))
+def test_prefill_attention_fp16_random_shapes(device, seed):
+    """Seeded sweep of the fp16 prefill kernel (128-vector query tiles over each sequence's blocks, causal mask)
+    against the oracle: batch 1-4, GQA ratio 1-8, 1-8 KV heads, pages of 16 or 32, 1-700 new tokens after 0-900
+    tokens of earlier context, so tiles end mid-token, sequences have different lengths and blocks end mid-page."""
+    from cacheir_amd import kernels
+
+    rng = np.random.default_rng(4000 + seed)
+    batch = int(rng.integers(1, 5))
+    g = int(rng.integers(1, 9))
+    hkv = int(rng.choice([1, 2, 4, 8]))
+    psize = int(rng.choice([16, 32]))
+    q_len = int(rng.choice([2, 7, 33, 129, int(rng.integers(1, 701))]))
+    past = rng.integers(0, 901, batch)
+    total = past + q_len
+    kp, vp, pt, lens = paged.build_pool(rng, total, hkv, 128, psize)
+    hq = g * hkv
+    q = rng.standard_normal((batch * q_len, hq, 128)).astype(np.float16)
+    out = kernels.paged_prefill_attention(to_dev(q, device), to_dev(kp, device), to_dev(vp, device), to_dev(pt, device),
+                                          to_dev(lens, device), q_len, check_tables=True).float().cpu().numpy()
+    for b in range(batch):
+        kh = paged.gather_sequence(kp, pt[b], int(total[b])).astype(np.float32)[None]
+        vh = paged.gather_sequence(vp, pt[b], int(total[b])).astype(np.float32)[None]
+        qh = q[b * q_len:(b + 1) * q_len].astype(np.float32)[None]
+        ref = ops.attention(qh, kh, vh, hq, hkv, 128, causal=True).reshape(q_len, hq, 128)
+        close16(out[b * q_len:(b + 1) * q_len], ref)
+
+
 # -------------------------------------------------------------- block weights --
 @pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
 def test_dequant_bit_exact(device, fmt):

@@ -125,7 +125,9 @@ int cir_paged_decode_attention_qkv_parts(const float* qkv_partial, int splits, c
 /* Causal prefill over the same paged pool (reference prefill attention semantics,
  * cacheir/runtime/cpu.py:361-368): q is [batch * q_len, num_heads, head_dim]; row
  * (b, s) attends to tokens t < seq_lens[b] - q_len + s + 1, where seq_lens[b] is the
- * length after the q_len new tokens were appended. */
+ * length after the q_len new tokens were appended.  On the fp16 head_dim-128 path
+ * (q_len > 1) the workspace is checked but not written: 128 query vectors of a sequence
+ * share each K/V block read and the output is written directly. */
 int cir_paged_prefill_attention(const void* q, const void* k_pool, const void* v_pool,
                                 const int32_t* page_table, const int32_t* seq_lens, void* out,
                                 void* workspace, size_t workspace_bytes,

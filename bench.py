@@ -28,7 +28,9 @@ config 3's 14336 -> 4096 and 4096 -> 14336 projections, rotated over the layers'
 takes the MFMA GEMM), the batched GEMM
 on MFMA (BASELINE config 5's Q8_0 gate|up + SwiGLU at batch 128: TFLOP/s against the dense fp16
 MFMA peak), the same decode
-step at batch 1 (decode_batch1: the projections and greedy head then run the GEMV), and a CPU
+step at batch 1 (decode_batch1: the projections and greedy head then run the GEMV), BASELINE config 5's
+full decode step (decode_config5: Qwen2-7B shape, Q8_0, batch 128 over a shared 1024-token prefix and ragged
+suffixes, against its HBM floor of unique bytes), and a CPU
 baseline (the C/OpenMP oracle restatement timed on this
 host over one layer and the lm_head, scaled to a full step).
 
@@ -120,6 +122,14 @@ def llama3_8b(layers: int):
     return ModelConfig(architecture="Llama3-8B-shape", hidden_size=4096, intermediate_size=14336, num_layers=layers,
                        num_attention_heads=32, num_key_value_heads=8, vocab_size=128256,
                        max_position_embeddings=8192, rope_theta=500000.0, rms_norm_eps=1e-5, dtype="float16")
+
+
+def qwen2_7b(layers: int):
+    from cacheir_amd.artifact import ModelConfig
+
+    return ModelConfig(architecture="Qwen2-7B-shape", hidden_size=3584, intermediate_size=18944, num_layers=layers,
+                       num_attention_heads=28, num_key_value_heads=4, vocab_size=152064,
+                       max_position_embeddings=32768, rope_theta=1000000.0, rms_norm_eps=1e-6, dtype="float16")
 
 
 def graph_us_per_launch(launch, iters: int, replays: int = 3, warm_replays: int = 2) -> float:
@@ -311,6 +321,74 @@ def prefill_case(base, cfg, tokens: int, dev) -> dict:
     return {"tokens": tokens, "batch": 1, "ms": round(ms, 3), "tokens_per_s": round(tokens / ms * 1e3, 1),
             "tflops": round(tflops, 1), "frac_mfma": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
             "note": "HipRuntime.run(mode='prefill') wall time, host launches included; logits for every position"}
+
+
+def config5_step_case(dev, steps: int, warmup: int) -> dict:
+    """BASELINE config 5's full decode step: the Qwen2-7B shape (28 layers, Q8_0, random-init: int8 uniform,
+    d = |N(0, 3e-4)|, so weights have std ~0.02), batch 128; one 1024-token prefix in 64 pages that every page
+    table shares (forks aliasing the base session's pages, no copies), suffixes U[64, 7168] (numpy seed 0, the
+    draw of the config-5 attention case) in pages of each session's own lane; N(0, 1) fp16 K/V.  The greedy step
+    (fused LM head + argmax) captured in a HIP graph, as for config 4.  The HBM floor counts every weight once and
+    the K/V of the prefix once per layer (the unique bytes)."""
+    import torch
+
+    from cacheir_amd.compiler import compile_config
+    from cacheir_amd.runtime import HipRuntime
+    from cacheir_amd.weights import GGML_Q8_0, SyntheticQuant
+
+    B, prefix, P = 128, 1024, 16
+    cfg = qwen2_7b(28)
+    sfx = np.random.default_rng(0).integers(64, 7169, B)
+    t0 = time.time()
+    art = compile_config(cfg, quant="q8_0", modes=("decode",))
+    pages = prefix // P + int((-(-sfx // P)).sum()) + 33 * 8
+    base = HipRuntime(art, source=SyntheticQuant(GGML_Q8_0, dev, seed=0, scale_sigma=3e-4), kv_capacity_pages=pages)
+    base.kv_cache.ensure_capacity(prefix)
+    base.kv_cache.tokens = prefix
+    sessions = []
+    for n in sfx:
+        s = base.fork()
+        s.kv_cache.alias_prefix(base.kv_cache.slots, prefix)
+        s.kv_cache.ensure_capacity(prefix + int(n))
+        s.kv_cache.tokens = prefix + int(n) - 1
+        sessions.append(s)
+    g = torch.Generator(device=dev)
+    g.manual_seed(5)
+    for layer in range(cfg.num_layers):
+        base.kv_allocator.k[layer].normal_(generator=g)
+        base.kv_allocator.v[layer].normal_(generator=g)
+    max_pages = base._bucket(max(len(s.kv_cache.slots) for s in sessions))
+    plan = base.plan("decode", B, 1, max_pages)
+    rows = np.zeros((B, max_pages), np.int32)
+    for b, s in enumerate(sessions):
+        rows[b, : len(s.kv_cache.slots)] = s.kv_cache.slots
+    ids = np.random.default_rng(1).integers(0, cfg.vocab_size, size=(B, 1))
+    plan.set_inputs(ids, rows, np.array([s.kv_cache.tokens for s in sessions], np.int32))
+    plan.launch_with_argmax()
+    torch.cuda.synchronize()
+    assert torch.isfinite(plan.logits).all().item(), "config 5: non-finite logits"
+    want = plan.next_ids.clone()
+    plan.next_ids.zero_()
+    plan.launch_greedy()
+    torch.cuda.synchronize()
+    assert torch.equal(plan.next_ids, want), "config 5: fused greedy head disagrees with argmax(logits)"
+    log(f"config 5 model ready in {time.time() - t0:.1f}s; weights {base.weights.nbytes() / 1e9:.3f} GB")
+    ms = time_greedy_steps(plan, steps, warmup)
+    embed = base.weights.dense("tok_embeddings", torch.float16)
+    weight_bytes = base.weights.nbytes() - embed.numel() * embed.element_size() + B * cfg.hidden_size * 2
+    per_token = cfg.num_layers * 2 * cfg.num_key_value_heads * cfg.head_dim * 2  # K + V over all layers
+    unique = per_token * (prefix + int(sfx.sum()))
+    logical = per_token * int((prefix + sfx).sum())
+    floor_ms = (weight_bytes + unique) / HBM_PEAK_GBS / 1e6
+    res = {"workload": "BASELINE config 5: Qwen2-7B-shape Q8_0 full decode step, shared 1024-token prefix",
+           "batch": B, "layers": cfg.num_layers, "context_sum": int((prefix + sfx).sum()),
+           "context_max": int((prefix + sfx).max()), "ms_per_step": round(ms, 4),
+           "tokens_per_s": round(B * 1000.0 / ms, 2), "weight_bytes": weight_bytes, "kv_unique_bytes": unique,
+           "kv_logical_bytes": logical, "hbm_floor_ms": round(floor_ms, 4), "frac_of_floor": round(floor_ms / ms, 4),
+           "gemm_plans": base.cache_stats()["gemm_plans"]}
+    del plan, sessions, base, embed
+    torch.cuda.empty_cache()
+    return res
 
 
 def gemm_rooflines(base, cfg, B, dev, args) -> dict:
@@ -514,6 +592,9 @@ def main() -> int:
     log(f"prefill {prefill['tokens']} tokens {prefill['ms']:.2f} ms -> {prefill['tokens_per_s']:.0f} tok/s, "
         f"{prefill['tflops']:.0f} TFLOP/s ({prefill['frac_mfma']:.1%} of fp16 MFMA)")
     gemm_plans = base.cache_stats()["gemm_plans"]
+    c5 = config5_step_case(dev, args.steps, args.warmup)
+    log(f"config 5 step {c5['ms_per_step']:.3f} ms -> {c5['tokens_per_s']:.1f} tok/s "
+        f"({c5['frac_of_floor']:.1%} of its {c5['hbm_floor_ms']:.2f} ms HBM floor)")
 
     traffic = measured_traffic(TRAFFIC_FILE)
 
@@ -570,6 +651,7 @@ def main() -> int:
                           "hbm_floor_ms": round((weight_bytes + kv_b1) / HBM_PEAK_GBS / 1e6, 4),
                           "note": "same model and context, one sequence; projections on the dequant GEMV"},
         "prefill": prefill,
+        "decode_config5": c5,
         "runtime_api_steps": {"note": "wall ms per step through HipRuntime.decode_greedy / run_decode_batch (+ "
                                       "synchronize), host work included, graph replay per step",
                               **host_steps},

@@ -15,6 +15,13 @@
 Weights are given as a dict ``value name -> float32 array`` (GGUF Q4_0/Q8_0 weights
 already decoded to float32 as ``gguf.py`` does at load).
 
+Rows of one batch may hold different lengths (a ragged decode batch, as a scheduler
+forms from sessions at different positions): ``keys[layer]`` / ``values[layer]`` are
+then lists of per-row ``[T_b, Hkv, D]`` arrays.  Each row's RoPE offset is its own
+length (``ops.rope_offsets``, ``cuda.py:1084-1102``) and its attention runs over its own
+cache; the matmuls run over the whole batch.  Row ``b`` gives what a session holding
+only that row computes (pinned against ``decode_batch`` in the CPU tests).
+
 ``OracleRuntime(..., fp16_storage=True)`` rounds values to float16 where a float16
 backend stores them (every matmul input, i.e. the normalised activations, the
 attention output and the SwiGLU output; q, k and v after RoPE, k and v as they enter
@@ -84,7 +91,16 @@ class OracleRuntime:
         return other
 
     def kv_length(self, layer: int) -> int:
+        if isinstance(self.keys.get(layer), list):
+            raise ValueError(f"the rows of layer {layer}'s cache hold different lengths (a ragged cache)")
         return int(self.keys[layer].shape[1]) if layer in self.keys else 0
+
+    def _rope(self, x: np.ndarray, layer: int, hd: int, theta: float) -> np.ndarray:
+        """RoPE at the layer's cache length: one offset for a uniform cache, one per row for a ragged one."""
+        kk = self.keys.get(layer)
+        if isinstance(kk, list):
+            return ops.rope_offsets(x, hd, theta, [len(r) for r in kk])
+        return ops.rope_one(x, hd, theta, self.kv_length(layer))
 
     def run(self, input_ids, *, mode: str = "prefill", reset_kv: bool | None = None) -> np.ndarray:
         graph = self.graphs[mode]
@@ -131,19 +147,29 @@ class OracleRuntime:
         if op in {"fused_rmsnorm_qkv_rope", "quantized_fused_rmsnorm_qkv_rope"}:
             x = st(ops.rms_norm(env[ins[0]], env[ins[1]], float(attrs.get("eps", 1e-6))))
             q, k, v = ops.matmul(x, env[ins[2]]), ops.matmul(x, env[ins[3]]), ops.matmul(x, env[ins[4]])
-            off = self.kv_length(int(attrs.get("layer", 0)))
+            layer = int(attrs.get("layer", 0))
             hd, theta = int(attrs["head_dim"]), float(attrs.get("rope_theta", 10000.0))
-            return [st(ops.rope_one(q, hd, theta, off)), st(ops.rope_one(k, hd, theta, off)), st(v)]
+            return [st(self._rope(q, layer, hd, theta)), st(self._rope(k, layer, hd, theta)), st(v)]
         if op == "rope":
-            off = self.kv_length(int(attrs.get("layer", 0)))
+            layer = int(attrs.get("layer", 0))
             hd, theta = int(attrs["head_dim"]), float(attrs.get("rope_theta", 10000.0))
-            return [ops.rope_one(env[ins[0]], hd, theta, off), ops.rope_one(env[ins[1]], hd, theta, off)]
+            return [self._rope(env[ins[0]], layer, hd, theta), self._rope(env[ins[1]], layer, hd, theta)]
         if op in {"paged_attention_prefill", "paged_attention_decode", "grouped_query_attention"}:
             q, k, v = env[ins[0]], env[ins[1]], env[ins[2]]
             layer = int(attrs.get("layer", 0))
             heads, kvh, hd = int(attrs["num_heads"]), int(attrs["num_kv_heads"]), int(attrs["head_dim"])
             b, s, _ = q.shape
-            kh, vh = self._append(layer, k.reshape(b, k.shape[1], kvh, hd), v.reshape(b, v.shape[1], kvh, hd))
+            k4, v4 = k.reshape(b, k.shape[1], kvh, hd), v.reshape(b, v.shape[1], kvh, hd)
+            if isinstance(self.keys.get(layer), list):  # ragged: each row over its own cache
+                outs = []
+                for r in range(b):
+                    self.keys[layer][r] = np.concatenate([self.keys[layer][r], k4[r]], axis=0)
+                    self.values[layer][r] = np.concatenate([self.values[layer][r], v4[r]], axis=0)
+                    outs.append(ops.attention(q[r: r + 1].reshape(1, s, heads, hd), self.keys[layer][r][None],
+                                              self.values[layer][r][None], heads, kvh, hd,
+                                              causal=(mode == "prefill")))
+                return [np.concatenate(outs, axis=0)]
+            kh, vh = self._append(layer, k4, v4)
             return [ops.attention(q.reshape(b, s, heads, hd), kh, vh, heads, kvh, hd, causal=(mode == "prefill"))]
         if op == "add":
             return [env[ins[0]] + env[ins[1]]]

@@ -110,9 +110,9 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--gemm-iters", type=int, default=64)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first copy 256 MiB four times (the known-size kernel for FETCH_SIZE/WRITE_SIZE scaling)")
-    ap.add_argument("--only", choices=["gemm"], default=None,
-                    help="run only the projection rooflines (for rocprofv3 counter runs of the GEMM kernels) and "
-                         "print their JSON; not a bench line")
+    ap.add_argument("--only", choices=["gemm", "config5"], default=None,
+                    help="run only the projection rooflines (gemm) or only BASELINE config 5's decode step "
+                         "(config5), for rocprofv3 runs of those kernels, and print their JSON; not a bench line")
     return ap.parse_args()
 
 
@@ -477,6 +477,9 @@ def main() -> int:
         torch.cuda.synchronize()
         log(f"calibration: copied {src.numel() * 4} bytes x4")
         del src, dst
+    if args.only == "config5":
+        print(json.dumps({"only": "config5", **config5_step_case(dev, args.steps, args.warmup)}), flush=True)
+        return 0
     cfg = llama3_8b(args.layers)
     B, ctx, P = args.batch, args.ctx, 16
     art = compile_config(cfg, quant="q4_0", modes=("prefill", "decode"))

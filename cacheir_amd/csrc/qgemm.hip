@@ -657,6 +657,7 @@ __global__ __launch_bounds__(64 * W) void qgemm_xl_kernel(const f16* __restrict_
   const int split = blockIdx.y;
   const int m0 = blockIdx.z * 16 * MT;
   const int q0 = split * nq;
+  const int nqs = min(nq, KQ - q0);  // quads of this split (the last may hold fewer)
 
   // Activation DMA: instruction u (0..XU-1) of wavefront w fills LDS bytes
   // [(w*XU + u) KiB, +1 KiB) of a slot, 16 B per lane: row r = 4 (w*XU + u) + lane/16,
@@ -691,7 +692,7 @@ __global__ __launch_bounds__(64 * W) void qgemm_xl_kernel(const f16* __restrict_
   constexpr int R = DW + 1;
   WS ws[R];
   auto issue = [&](int slot, int idx) __attribute__((always_inline)) {  // quad idx, clamped to the last
-    const uint32_t Q = (uint32_t)min(idx, nq - 1);
+    const uint32_t Q = (uint32_t)min(idx, nqs - 1);
 #pragma unroll
     for (int b = 0; b < NT; ++b) {
 #pragma unroll
@@ -774,18 +775,18 @@ __global__ __launch_bounds__(64 * W) void qgemm_xl_kernel(const f16* __restrict_
   // wait before the barrier covers the DMA but not the weights issued after it.
   int i = 0;
 #pragma nounroll
-  for (; i + R <= nq; i += R) {
+  for (; i + R <= nqs; i += R) {
     each.template operator()<R>([&]<int S>() {
       compute(ws[S], (i + S) & 1);
-      dma_x((i + S + 1) & 1, min(i + S + 1, nq - 1));
+      dma_x((i + S + 1) & 1, min(i + S + 1, nqs - 1));
       issue((S + DW) % R, i + S + DW);
       barrier();
     });
   }
   each.template operator()<DW>([&]<int S>() {  // at most DW quads are left, in ring slots 0 .. DW-1
-    if (i + S < nq) {
+    if (i + S < nqs) {
       compute(ws[S], (i + S) & 1);
-      dma_x((i + S + 1) & 1, min(i + S + 1, nq - 1));
+      dma_x((i + S + 1) & 1, min(i + S + 1, nqs - 1));
       barrier();
     }
   });
@@ -1359,26 +1360,41 @@ constexpr int xl_mt(int m) { return m <= 64 ? 4 : 8; }
 // The partials launch keeps xl_mt (QKV, n 4608: 19.3 us at 64 rows against 16.4).
 constexpr int xl_mt_swiglu(int m) { return m <= 128 ? 4 : 8; }
 
-// m > 32 takes the large-m kernel when n spans at least 36 groups of 128 columns.
-// Measured at the Qwen2-7B shapes (Q8_0, m = 64 / 128) against the m <= 32 kernel
-// run over 32-row blocks: QKV (n 4608) 11.0 / 16.9 us against 15.4 / 24.5, gate|up
-// (n 37888) 51.6 / 81.8 against 72.6 / 114.9; but O and down (n 3584, 28 groups)
-// lose (O 14.3 against 13.4 us at m = 128, down 79 against 56): too few column
-// groups to fill the CUs without many more k-splits.
-bool use_xl(int m, int n) { return m > 32 && (n + 127) / 128 >= 36; }
+// Workgroups of the large-m kernel before any k-split: groups of 128 columns x blocks of 16*MT rows.
+long xl_groups(int m, int n) { return (long)((n + 127) / 128) * ((m + 16 * xl_mt(m) - 1) / (16 * xl_mt(m))); }
 
-// Its k-split: the smallest divisor of k/128 (not only powers of two) giving >= 192
-// workgroups, keeping at least 4 quads per split.
+// m > 32 takes the large-m kernel when n spans at least 36 groups of 128 columns, when
+// its workgroups alone fill the CUs (>= 192: large m), or, where k may be split, when k
+// holds at least 64 quads (the k-split pieces then stay long).  Measured at the Qwen2-7B
+// shapes (Q8_0, m = 64 / 128) against the m <= 32 kernel run over 32-row blocks: QKV
+// (n 4608) 11.0 / 16.9 us against 15.4 / 24.5, gate|up (n 37888) 51.6 / 81.8 against
+// 72.6 / 114.9; down (n 3584, 28 groups, k 18944) at m = 128: 42.3 us over 9 splits
+// against 49.1 / 66.4 for the small kernel at 4 / 2 splits; O (n 3584, k 3584: 28 quads)
+// stays on the small kernel (12.4-12.7 us against 14.6 at 7 splits).  At m = 2048
+// (Llama-3-8B, Q4_0) the large kernel takes down 353.8 -> 287.8 us and O 113.8 -> 95.2.
+// The SwiGLU launch cannot split k (splittable = false).
+bool use_xl(int m, int n, int k, bool splittable = true) {
+  if (m <= 32) return false;
+  return (n + 127) / 128 >= 36 || xl_groups(m, n) >= 192 || (splittable && k / 128 >= 64);
+}
+
+// Its k-split: as many splits as keep the launch at one round of workgroups over the
+// 256 CUs (down at m = 128: 9 splits, 252 workgroups: 42.3 us against 46.5 at 8 and 43.9
+// at 10), each split at least 4 quads.  The splits need not divide k/128: split s covers
+// quads s * ceil(kq / S) onward, the last one fewer.
 int xl_splits(int m, int n, int k) {
+  const long by_cus = 256 / xl_groups(m, n), by_len = (k / 128) / 4;
+  const long s = by_cus < by_len ? by_cus : by_len;
+  return s > 1 ? (int)s : 1;
+}
+
+// The k-splits a cir_qgemm launch accepts: those dividing k/128, and on the large-m
+// kernel any count whose every split holds at least one quad.
+bool splits_ok(int m, int n, int k, int splits) {
   const int kq = k / 128;
-  const long groups = (long)((n + 127) / 128) * ((m + 16 * xl_mt(m) - 1) / (16 * xl_mt(m)));
-  int best = 1;
-  for (int s = 1; s <= kq / 4; ++s) {
-    if (kq % s) continue;
-    best = s;
-    if (groups * s >= 192) break;
-  }
-  return best;
+  if (splits < 1 || splits > kq) return false;
+  if (kq % splits == 0) return true;
+  return use_xl(m, n, k) && (splits - 1) * ((kq + splits - 1) / splits) < kq;
 }
 
 #ifndef CIR_XL_W
@@ -1392,7 +1408,7 @@ void launch_qgemm_xl(const f16* x, int ldx, const uint8_t* wq, const uint16_t* w
   const int NTILES = (N + 15) / 16;
   dim3 grid((NTILES + 2 * W - 1) / (2 * W), splits, (M + 16 * MT - 1) / (16 * MT));
   qgemm_xl_kernel<FMT, MT, DW, EPI, TO, W>
-      <<<grid, 64 * W, 0, s>>>(x, ldx, wq, wd, part, M, N, K, (K / 128) / splits, act);
+      <<<grid, 64 * W, 0, s>>>(x, ldx, wq, wd, part, M, N, K, (K / 128 + splits - 1) / splits, act);
 }
 
 // Workgroup rows: 4 wavefronts x NT tiles x 16.  m <= 16 takes NT = 1 (64 rows per
@@ -1407,7 +1423,7 @@ int default_splits(int m, int n, int k) {
   if (m <= 8) {
     if (const int s = gemv_splits(m, n, k)) return s;
   }
-  if (use_xl(m, n)) return xl_splits(m, n, k);
+  if (use_xl(m, n, k)) return xl_splits(m, n, k);
   const int kq = k / 128;
   const long groups = (long)((n + xs_rows_per_group(m) - 1) / xs_rows_per_group(m)) * ((m + 31) / 32);
   int s = 1;
@@ -1420,7 +1436,7 @@ void dispatch_qgemm(const f16* x, int ldx, const uint8_t* wq, const uint16_t* wd
                     int splits, hipStream_t s) {
   if (gemv_fits(M, K, splits)) launch_qgemv<FMT, 0>(x, ldx, wq, wd, part, M, N, K, splits, s);
   else if (M <= 16) launch_qgemm_xs<FMT, 1, 1, 4>(x, ldx, wq, wd, part, M, N, K, splits, s);
-  else if (!use_xl(M, N)) launch_qgemm_xs<FMT, 2, 2, CIR_XS_DW>(x, ldx, wq, wd, part, M, N, K, splits, s);
+  else if (!use_xl(M, N, K)) launch_qgemm_xs<FMT, 2, 2, CIR_XS_DW>(x, ldx, wq, wd, part, M, N, K, splits, s);
   else if (M <= 64) launch_qgemm_xl<FMT, 4, 0>(x, ldx, wq, wd, part, M, N, K, splits, s);
   else launch_qgemm_xl<FMT, 8, 0>(x, ldx, wq, wd, part, M, N, K, splits, s);
 }
@@ -1504,7 +1520,9 @@ extern "C" int cir_qgemm(const void* x, int ldx, const void* w_tiled, int fmt, f
   CIR_CHECK_ARG(m >= 0 && n >= 0 && k >= 0, "qgemm: negative size");
   if (m == 0 || n == 0) return 0;
   CIR_CHECK_ARG(k > 0 && k % 128 == 0, "qgemm: k (%d) must be a positive multiple of 128", k);
-  CIR_CHECK_ARG(splits >= 1 && (k / 128) % splits == 0, "qgemm: splits (%d) must divide k/128 (%d)", splits, k / 128);
+  CIR_CHECK_ARG(splits_ok(m, n, k, splits),
+                "qgemm: splits (%d) must divide k/128 (%d), or on the large-m kernel leave no split empty", splits,
+                k / 128);
   CIR_CHECK_ARG(ldx >= k && ldx % 8 == 0, "qgemm: ldx (%d) must be >= k and a multiple of 8", ldx);
   CIR_CHECK_ARG(x && w_tiled && y_partial, "qgemm: null pointer");
   CIR_CHECK_ARG(splits <= 65535 && (m + 15) / 16 <= 65535, "qgemm: grid too large");
@@ -1569,7 +1587,7 @@ extern "C" int cir_qgemm_swiglu(const void* x, int ldx, const void* w_tiled, int
   const f16* xh = static_cast<const f16*>(x);
   hipStream_t s = as_stream(stream);
   auto go = [&]<int FMT>() {
-    if (use_xl(m, n)) {
+    if (use_xl(m, n, k, false)) {
       auto xl = [&]<int MT>() {
         if (odt == CIR_F16) launch_qgemm_xl<FMT, MT, 1, f16>(xh, ldx, q, d, nullptr, m, n, k, 1, s, static_cast<f16*>(out));
         else launch_qgemm_xl<FMT, MT, 1, float>(xh, ldx, q, d, nullptr, m, n, k, 1, s, static_cast<float*>(out));
@@ -1652,13 +1670,13 @@ extern "C" const char* cir_qgemm_plan(int op, int fmt, int m, int n, int k, int 
   if (!valid_fmt(fmt) || m <= 0 || n <= 0 || k <= 0 || k % 128) return "invalid";
   switch (op) {
     case CIR_GEMM_PARTIALS:
-      if (splits < 1 || (k / 128) % splits) return "invalid";
+      if (!splits_ok(m, n, k, splits)) return "invalid";
       if (gemv_fits(m, k, splits)) return "qgemv_kernel";
       if (m <= 16) return "qgemm_xs_kernel<NT=1,MT=1>";
-      if (!use_xl(m, n)) return "qgemm_xs_kernel<NT=2,MT=2>";
+      if (!use_xl(m, n, k)) return "qgemm_xs_kernel<NT=2,MT=2>";
       return m <= 64 ? "qgemm_xl_kernel<MT=4>" : "qgemm_xl_kernel<MT=8>";
     case CIR_GEMM_SWIGLU:
-      if (use_xl(m, n))
+      if (use_xl(m, n, k, false))
         return xl_mt_swiglu(m) == 4 ? "qgemm_xl_kernel<MT=4,EPI=swiglu>" : "qgemm_xl_kernel<MT=8,EPI=swiglu>";
       return m <= 16 ? "qgemm_xs_kernel<NT=2,MT=1,EPI=swiglu>" : "qgemm_xs_kernel<NT=2,MT=2,EPI=swiglu>";
     case CIR_GEMM_ARGMAX:

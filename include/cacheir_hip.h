@@ -160,9 +160,10 @@ int cir_qweight_repack_rows(const void* packed, const float* scales, const int32
  * tiled copy (tiled = 1).  Replaces gguf.py:273-310 for device-resident weights. */
 int cir_dequant(const void* weights, int tiled, int fmt, float* out, int n, int k, void* stream);
 
-/* The k-split cir_qgemm is tuned for at this shape (a power of two dividing k/128):
- * enough workgroups to fill the GPU, no more partials than that needs (for m <= 8,
- * the split under which the GEMV gives every CU the same share of the weights).
+/* The k-split cir_qgemm is tuned for at this shape: enough workgroups to fill the GPU,
+ * no more partials than that needs (for m <= 8, the split under which the GEMV gives
+ * every CU the same share of the weights; on the large-m GEMM, one round of workgroups
+ * over the CUs, which need not divide k/128).
  * 0 for an invalid shape.  (The reference has no k-split; this replaces its GEMM plan choice,
  * cacheir/runtime/cuda.py:956-974 _select_gemm_plan.) */
 int cir_qgemm_splits(int m, int n, int k);
@@ -176,7 +177,9 @@ size_t cir_qgemm_workspace_bytes(int m, int n, int splits);
  * m <= 8 with m * (k/128/splits) <= 128 runs the dequant GEMV (activations staged in
  * LDS once per workgroup, each wavefront streaming whole tiles); larger m the MFMA
  * GEMM.  For the same split both give the same partials bit for bit.
- * splits must divide k/128.  Requires k % 128 == 0. */
+ * splits must divide k/128, except where the large-m GEMM runs (cir_qgemm_plan names
+ * qgemm_xl_kernel): there split s covers quads s*ceil(k/128/splits) onward (the last
+ * fewer) and any count that leaves no split empty is taken.  Requires k % 128 == 0. */
 int cir_qgemm(const void* x, int ldx, const void* w_tiled, int fmt, float* y_partial,
               int m, int n, int k, int splits, void* stream);
 

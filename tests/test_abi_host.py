@@ -51,6 +51,34 @@ def test_library_loads_and_reports_version_without_a_gpu():
     assert lib.cir_paged_attention_workspace_bytes(2, 8, 128, 2048) > 0
 
 
+@pytest.mark.skipif(not hip.library_path().exists(), reason="libcacheir_hip.so not built")
+def test_gemm_planner_splits_and_kernels_without_a_gpu():
+    """The planner's choices are host arithmetic: the large-m kernel takes k-splits that need not divide k/128
+    (none empty), the m <= 32 kernel only divisors."""
+    from cacheir_amd import kernels
+
+    q8, q4, P = hip.CIR_Q8_0, hip.CIR_Q4_0, hip.GEMM_PARTIALS
+    # Qwen2-7B down at m = 128: 148 quads over 9 splits (17 each, the last 12), one round of 252 workgroups
+    assert kernels.choose_splits(128, 3584, 18944) == 9
+    assert kernels.gemm_plan(P, q8, 128, 3584, 18944, 9) == "qgemm_xl_kernel<MT=8>"
+    # its O (28 quads) stays on the small kernel, whose splits must divide k/128
+    assert kernels.gemm_plan(P, q8, 128, 3584, 3584, 2).startswith("qgemm_xs_kernel")
+    assert kernels.gemm_plan(P, q8, 128, 3584, 3584, 3) == "invalid"
+    # QKV keeps 7 splits of 4 quads (36 column groups)
+    assert kernels.choose_splits(128, 4608, 3584) == 7
+    # 64 quads over 9 splits would leave the last empty; over 10 the last holds one quad
+    assert kernels.gemm_plan(P, q8, 128, 100, 8192, 9) == "invalid"
+    assert kernels.gemm_plan(P, q8, 128, 100, 8192, 10) == "qgemm_xl_kernel<MT=8>"
+    # a 2048-token prefill fills the CUs with row blocks alone: large-m kernel, one split, for every projection
+    for n, k in ((6144, 4096), (4096, 4096), (4096, 14336), (128256, 4096)):
+        assert kernels.choose_splits(2048, n, k) == 1
+        assert kernels.gemm_plan(P, q4, 2048, n, k, 1) == "qgemm_xl_kernel<MT=8>", (n, k)
+    assert kernels.gemm_plan(hip.GEMM_SWIGLU, q4, 2048, 28672, 4096, 1) == "qgemm_xl_kernel<MT=8,EPI=swiglu>"
+    # decode at m = 32 is untouched: divisor splits on the small kernel
+    assert kernels.gemm_plan(P, q4, 32, 4096, 14336, 8).startswith("qgemm_xs_kernel")
+    assert kernels.gemm_plan(P, q4, 32, 4096, 14336, 9) == "invalid"
+
+
 def llama(layers=3, **kw):
     base = dict(architecture="LlamaForCausalLM", hidden_size=256, intermediate_size=512, num_layers=layers,
                 num_attention_heads=8, num_key_value_heads=2, vocab_size=1000, rope_theta=10000.0, rms_norm_eps=1e-5,

@@ -306,6 +306,35 @@ def test_qgemv_every_small_batch(device, fmt):
     close16(got, ops.matmul(x.astype(np.float32), dec(blocks, 4096)))
 
 
+@pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
+@pytest.mark.parametrize("m,n,k,splits", [(128, 100, 8192, 10), (40, 64, 8448, 7), (128, 3584, 18944, 9),
+                                          (70, 200, 8320, 4)])
+def test_qgemm_large_m_ragged_splits(device, fmt, m, n, k, splits):
+    """The large-m kernel's k-splits need not divide k/128: split s covers quads s * ceil(kq / S) onward and the
+    last one fewer (down to one quad).  Each split's partials against the exact-product bound of fp64 over that
+    range, and their sum against the oracle."""
+    from cacheir_amd import hip, kernels
+
+    code = kernels.FMT_NAMES[fmt]
+    assert kernels.gemm_plan(hip.GEMM_PARTIALS, code, m, n, k, splits).startswith("qgemm_xl_kernel")
+    rng = np.random.default_rng(m + n + k + splits)
+    enc, dec = (quant.random_q4_0, quant.decode_q4_0) if fmt == "q4_0" else (quant.random_q8_0, quant.decode_q8_0)
+    blocks = enc(rng, n, k)[0]
+    wf = dec(blocks, k).astype(np.float64)
+    w = kernels.QWeight.from_blocks(to_dev(blocks.reshape(-1), device), code, n, k)
+    x = rng.standard_normal((m, k)).astype(np.float16)
+    part = kernels.qgemm_partial(to_dev(x, device), w, splits=splits).double().cpu().numpy()
+    kq = k // 128
+    per = -(-kq // splits)
+    for s in range(splits):
+        lo, hi = 128 * s * per, 128 * min(kq, (s + 1) * per)
+        assert hi > lo
+        xs, ws_ = x[:, lo:hi].astype(np.float64), wf[:, lo:hi]
+        bound = 1e-5 * (np.abs(xs) @ np.abs(ws_).T) + 1e-6
+        assert np.all(np.abs(part[s] - xs @ ws_.T) <= bound), s
+    close16(part.sum(0), ops.matmul(x.astype(np.float32), wf.astype(np.float32)))
+
+
 def test_gemm_f32(device):
     from cacheir_amd import kernels
 
@@ -544,7 +573,7 @@ def test_qgemm_swiglu_matches_gemm_then_epilogue(device, fmt, m, k):
 @pytest.mark.parametrize("proj,n,k", [("qkv", 4608, 3584), ("down", 3584, 18944), ("gate_up", 18944, 3584)])
 def test_config5_projections_full_size(device, proj, n, k):
     """BASELINE config 5's Q8_0 projections at batch 128, full Qwen2-7B shapes: QKV (the large-m kernel), down
-    (n spans 28 column groups: the m <= 32 kernel in four row blocks) and gate|up with the fused SwiGLU, against the
+    (the large-m kernel over 9 k-splits of 17 quads, the last 12) and gate|up with the fused SwiGLU, against the
     dequantized oracle.  Scales are |N(0, 5e-4)| so that int8 codes give weights of config 3's size (RMS ~0.03);
     with config 3's 0.01, |g| and |u| reach ~150 and fp32 accumulation alone moves silu(g) * u by ~2e-3."""
     from cacheir_amd import kernels

@@ -639,13 +639,15 @@ __device__ __forceinline__ void buf16_to_lds(rsrc_t r, uint8_t* lds, uint32_t vo
 // DW + 1 slots as in the GEMV.  Per tile and quad the blocks are scaled and summed in
 // the m <= 32 kernel's order, so for the same split both give the same bits.
 // EPI 0: fp32 split-k partials part[split][m][n]; EPI 1: SwiGLU over interleaved
-// gate/up tiles (one split), out[m][N/2] in type TO.
+// gate/up tiles (one split), out[m][N/2] in type TO; EPI 2: greedy-head candidates
+// (one split), the best column of each wavefront's 32 and row: value in part, index in
+// act (as int), at [m][blockIdx.x * W + wave], for argmax_cand_kernel.
 template <int FMT, int MT, int DW, int EPI = 0, typename TO = float, int W = 4>
 __global__ __launch_bounds__(64 * W) void qgemm_xl_kernel(const f16* __restrict__ x, int ldx,
                                                      const uint8_t* __restrict__ wq, const uint16_t* __restrict__ wd,
                                                      float* __restrict__ part, int M, int N, int K, int nq,
                                                      TO* __restrict__ act = nullptr) {
-  static_assert(EPI == 0 || EPI == 1, "large-m GEMM epilogues: partials or SwiGLU");
+  static_assert(EPI >= 0 && EPI <= 2, "large-m GEMM epilogues: partials, SwiGLU or argmax candidates");
   constexpr int NT = 2;
   constexpr int LB = Stage<FMT, NT, 1>::LB;
   constexpr int kSlot = 16 * MT * 256;  // bytes of one quad of activations
@@ -810,7 +812,36 @@ __global__ __launch_bounds__(64 * W) void qgemm_xl_kernel(const f16* __restrict_
         for (int r = 0; r < 4; ++r) acc[a][b][r] = sc * fmaf(of, sx[a][r], acc[a][b][r]);
     }
   }
-  if constexpr (EPI == 1) {
+  if constexpr (EPI == 2) {
+    float* cand_v = part;
+    int* cand_i = reinterpret_cast<int*>(act);
+    const int wv_global = blockIdx.x * W + wave;
+    const int WT = gridDim.x * W;
+#pragma unroll
+    for (int a = 0; a < MT; ++a)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float bv = -INFINITY;
+        int bi = 0x7fffffff;
+#pragma unroll
+        for (int b = 0; b < NT; ++b) {
+          const int n = (nt0 + b) * 16 + li;
+          if (nt0 + b < NTILES && n < N) argmax_better(bv, bi, acc[a][b][r], n);
+        }
+        // the 16 lanes of this row group (same lg) hold 16 different columns
+#pragma unroll
+        for (int off = 8; off > 0; off >>= 1) {
+          const float ov = __shfl_xor(bv, off, 64);
+          const int oi = __shfl_xor(bi, off, 64);
+          argmax_better(bv, bi, ov, oi);
+        }
+        const int m = m0 + 16 * a + 4 * lg + r;
+        if (li == 0 && m < M) {
+          cand_v[(size_t)m * WT + wv_global] = bv;
+          cand_i[(size_t)m * WT + wv_global] = bi;
+        }
+      }
+  } else if constexpr (EPI == 1) {
     const int inter = N / 2;
     const int col = (nt0 >> 1) * 16 + li;
     if (nt0 + 1 < NTILES && col < inter) {
@@ -1411,6 +1442,24 @@ void launch_qgemm_xl(const f16* x, int ldx, const uint8_t* wq, const uint16_t* w
       <<<grid, 64 * W, 0, s>>>(x, ldx, wq, wd, part, M, N, K, (K / 128 + splits - 1) / splits, act);
 }
 
+// The fused greedy head on the large-m kernel (one split): 128 columns per workgroup, one
+// candidate per wavefront and row, as many as argmax_cand_count gives the m > 16 kernel.
+// At the Qwen2-7B head (n 152064, k 3584, Q8_0) it reads the weights once per 16*MT rows
+// where the m <= 32 kernel reads them once per 32: 495.6 us at m = 128 for the latter
+// against 268.6 us for the large-m kernel's logits alone.
+template <int FMT, int MT>
+void launch_qgemm_xl_argmax(const f16* x, int ldx, const uint8_t* wq, const uint16_t* wd, float* cand_v, int* cand_i,
+                            int64_t* ids, int M, int N, int K, hipStream_t s) {
+  constexpr int DW = layout_fmt(FMT) == CIR_Q4_0 ? 4 : 3;
+  constexpr int W = CIR_XL_W;
+  static_assert(2 * 16 * W == 128, "argmax_cand_count assumes 128 columns per workgroup");
+  const int NTILES = (N + 15) / 16;
+  dim3 grid((NTILES + 2 * W - 1) / (2 * W), 1, (M + 16 * MT - 1) / (16 * MT));
+  qgemm_xl_kernel<FMT, MT, DW, 2, float, W>
+      <<<grid, 64 * W, 0, s>>>(x, ldx, wq, wd, cand_v, M, N, K, K / 128, reinterpret_cast<float*>(cand_i));
+  argmax_cand_kernel<<<M, 256, 0, s>>>(cand_v, cand_i, (int)grid.x * W, M, ids);
+}
+
 // Workgroup rows: 4 wavefronts x NT tiles x 16.  m <= 16 takes NT = 1 (64 rows per
 // workgroup, MT = 1); larger m takes NT = 2, MT = 2 (128 rows x 32 activation rows):
 // each activation quad then feeds 8 weight tiles.  Measured on MI355X at the
@@ -1656,8 +1705,14 @@ extern "C" int cir_qgemm_argmax(const void* x, int ldx, const void* w_tiled, int
         return;
       }
     }
-    if (m <= 16) launch_qgemm_argmax<FMT, 1, 1>(xh, ldx, q, d, cv, ci, ids, m, n, k, s);
-    else launch_qgemm_argmax<FMT, 2, 2>(xh, ldx, q, d, cv, ci, ids, m, n, k, s);
+    if (use_xl(m, n, k, false)) {
+      if (m <= 64) launch_qgemm_xl_argmax<FMT, 4>(xh, ldx, q, d, cv, ci, ids, m, n, k, s);
+      else launch_qgemm_xl_argmax<FMT, 8>(xh, ldx, q, d, cv, ci, ids, m, n, k, s);
+    } else if (m <= 16) {
+      launch_qgemm_argmax<FMT, 1, 1>(xh, ldx, q, d, cv, ci, ids, m, n, k, s);
+    } else {
+      launch_qgemm_argmax<FMT, 2, 2>(xh, ldx, q, d, cv, ci, ids, m, n, k, s);
+    }
   };
   if (fmt == CIR_Q4_0) go.template operator()<CIR_Q4_0>();
   else if (fmt == CIR_Q8_0) go.template operator()<CIR_Q8_0>();
@@ -1681,6 +1736,9 @@ extern "C" const char* cir_qgemm_plan(int op, int fmt, int m, int n, int k, int 
       return m <= 16 ? "qgemm_xs_kernel<NT=2,MT=1,EPI=swiglu>" : "qgemm_xs_kernel<NT=2,MT=2,EPI=swiglu>";
     case CIR_GEMM_ARGMAX:
       if (gemv_head_fits(fmt, m, k)) return "qgemv_kernel<EPI=argmax>+argmax_cand_kernel";
+      if (use_xl(m, n, k, false))
+        return m <= 64 ? "qgemm_xl_kernel<MT=4,EPI=argmax>+argmax_cand_kernel"
+                       : "qgemm_xl_kernel<MT=8,EPI=argmax>+argmax_cand_kernel";
       return m <= 16 ? "qgemm_xs_kernel<NT=1,MT=1,EPI=argmax>+argmax_cand_kernel"
                      : "qgemm_xs_kernel<NT=2,MT=2,EPI=argmax>+argmax_cand_kernel";
     case CIR_GEMM_ATTN_MERGE:

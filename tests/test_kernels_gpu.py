@@ -740,16 +740,18 @@ def test_row_kernels(device):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("fmt", ["q4_0", "q8_0", "i4_row", "i8_row"])
-@pytest.mark.parametrize("m,k", [(1, 256), (5, 256), (8, 256), (16, 256), (17, 256), (32, 256), (2, 4096), (8, 4096)])
+@pytest.mark.parametrize("m,k", [(1, 256), (5, 256), (8, 256), (16, 256), (17, 256), (32, 256), (2, 4096), (8, 4096),
+                                 (40, 256), (130, 384)])
 def test_qgemm_argmax_matches_gemm_then_argmax(device, fmt, m, k):
     """cir_qgemm_argmax (LM head + greedy argmax, no logits stored) == the oracle's greedy pick over the logits
     of cir_qgemm (splits 1): bitwise the same ids, with a planted tie between a near and a far column (first
     index wins), a row of NaN logits (numpy picks the first NaN, index 0) and a ragged vocabulary. Block formats
-    at m <= 8 run the GEMV's argmax epilogue, the rest the GEMM's."""
-    from cacheir_amd import kernels
+    at m <= 8 run the GEMV's argmax epilogue, m <= 32 the small GEMM's, and m > 32 over 37 column groups the
+    large-m GEMM's (64- and 128-row blocks, a ragged last block at m = 130)."""
+    from cacheir_amd import hip, kernels
 
     rng = np.random.default_rng(17 * m + len(fmt) + k)
-    n = 1000  # not a multiple of the 32- or 64-column wavefront groups
+    n = 1000 if m <= 32 else 4610  # not a multiple of the 32- or 64-column wavefront groups
     if fmt in ("q4_0", "q8_0"):
         enc = quant.random_q4_0 if fmt == "q4_0" else quant.random_q8_0
         blocks = enc(rng, n, k)[0].reshape(n, -1)
@@ -767,6 +769,8 @@ def test_qgemm_argmax_matches_gemm_then_argmax(device, fmt, m, k):
         pk = quant.asymmetric_pack(wf, bits)
         w = kernels.QWeight.from_rows(to_dev(pk["packed_values"], device), to_dev(pk["scales"], device),
                                       to_dev(pk["zero_points"], device), bits, n, k)
+    if m > 32:
+        assert kernels.gemm_plan(hip.GEMM_ARGMAX, w.fmt, m, n, k).startswith("qgemm_xl_kernel")
     x = np.abs(rng.standard_normal((m, k))).astype(np.float16)
     if m > 2:
         x[1] = rng.standard_normal(k).astype(np.float16)  # a row with an ordinary (random) winner

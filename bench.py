@@ -446,6 +446,9 @@ def gemm_rooflines(base, cfg, B, dev, args) -> dict:
     w5 = [random_q8_0(100 + i) for i in range(4)]  # 4 x 144 MB: rotated past the 256 MB MALL
     x5 = torch.randn((m5, k5), device=dev, dtype=torch.float16)
     o5 = torch.empty((m5, n5 // 2), device=dev, dtype=torch.float16)
+    from cacheir_amd import hip
+
+    plan5 = kernels.gemm_plan(hip.GEMM_SWIGLU, kernels.FMT_NAMES["q8_0"], m5, n5, k5)
     us5 = graph_us_per_launch(lambda it: kernels.qgemm_swiglu(x5, w5[it % len(w5)], out=o5), args.gemm_iters)
     tflops5 = 2.0 * m5 * n5 * k5 / (us5 * 1e-6) / 1e12
     gbs5 = (w5[0].nbytes + 2 * m5 * k5 + 2 * m5 * (n5 // 2)) / (us5 * 1e-6) / 1e9
@@ -453,7 +456,7 @@ def gemm_rooflines(base, cfg, B, dev, args) -> dict:
         f"({tflops5 / MFMA_F16_PEAK_TFLOPS:.1%} of fp16 MFMA), {gbs5:.0f} GB/s")
     del w5
     return {"us": gemm_us, "bytes": gemm_bytes, "gbs": gemm_gbs, "gemv": gemv, "us5": us5, "tflops5": tflops5,
-            "gbs5": gbs5}
+            "gbs5": gbs5, "plan5": plan5}
 
 
 def main() -> int:
@@ -643,11 +646,11 @@ def main() -> int:
                                                     "GEMV at m <= 8, MFMA GEMM at m = 32",
                           "peak": HBM_PEAK_GBS, "unit": "GB/s", "shapes": gemv},
         "roofline_batched_gemm": {"bound": "mfma",
-                                  "kernel": "Q8_0 gate|up GEMM + SwiGLU m=128 (qgemm_xl_kernel, EPI=1), "
+                                  "kernel": f"Q8_0 gate|up GEMM + SwiGLU m=128 ({gemm['plan5']}), "
                                             "BASELINE config 5 shape (n 37888, k 3584)",
                                   "achieved": round(tflops5, 1), "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
                                   "frac": round(tflops5 / MFMA_F16_PEAK_TFLOPS, 4), "us_per_launch": round(us5, 3),
-                                  "hbm_gbs": round(gbs5, 1), "counters": measured_counters(COUNTERS_FILE, "xl")},
+                                  "hbm_gbs": round(gbs5, 1), "counters": measured_counters(COUNTERS_FILE, "xw")},
         "step_bytes": {"weights": weight_bytes, "kv": kv_bytes * cfg.num_layers,
                        "hbm_floor_ms": round((weight_bytes + kv_bytes * cfg.num_layers) / HBM_PEAK_GBS / 1e6, 4)},
         "decode_batch1": {"ms_per_step": round(ms_b1, 4), "tokens_per_s": round(1000.0 / ms_b1, 2),

@@ -871,6 +871,210 @@ __global__ __launch_bounds__(64 * W) void qgemm_xl_kernel(const f16* __restrict_
   }
 }
 
+// Balanced large m (qgemm_xw_kernel): one workgroup of 4 wavefronts per CU, each
+// workgroup owning a contiguous run of 1..5 tile pairs (gate/up pairs for SwiGLU) and all
+// 16*MT rows of its row block, so the launch is one round over the CUs with every CU's
+// share of the columns within one pair of the mean (the large-m kernel's fixed 128-column
+// groups leave 2 or 3 workgroups per CU).  Per quad the weight codes and scales of the
+// run and the activations all go to LDS by buffer DMA, double-buffered in two separate
+// arrays so the compiler lets the LDS reads of one slot overlap the DMA into the other.
+// Wavefront w computes pair w over all rows and, in a 5-pair run, rows w*MT/4.. of the
+// fifth pair: each dequantized fragment feeds MT (or MT/4) MFMAs, and the four
+// wavefronts have the same MFMA count.  Per tile, quad and block the arithmetic is the
+// large-m kernel's in the same order, so for the same split both give the same bits.
+// EPI 0: fp32 partials part[split][m][n]; EPI 1: SwiGLU over interleaved gate/up tiles
+// (one split), out[m][N/2] in type TO.  Block formats only.
+constexpr int kXwPairs = 5;
+template <int FMT>
+inline constexpr int kXwTileBytes = 1024 * Stage<FMT, 1, 1>::LB;  // codes of one tile and quad
+// One slot: activations (16*MT rows x 256 B), codes of up to 10 tiles, then 2 KiB of
+// scales (two whole DMA instructions: tiles 0-7 and 8-9, the rest of the second unused).
+template <int FMT, int MT>
+inline constexpr int kXwSlot = 16 * MT * 256 + 2 * kXwPairs * kXwTileBytes<FMT> + 2048;
+
+template <int FMT, int MT, int W>
+__device__ __forceinline__ void xw_dma(uint8_t* slot, rsrc_t rx, rsrc_t rw, rsrc_t rd,
+                                       const uint32_t (&xoff)[4 * MT / W], int wave, int lane, int t0, int ntl, int KQ,
+                                       int Q) {
+  constexpr int TB = kXwTileBytes<FMT>, LB = TB / 1024;
+  constexpr int XB = 16 * MT * 256, XU = 4 * MT / W;
+  // activations: wavefront w brings KiB w*XU .. w*XU+XU-1 of the quad (rows 4 KiB-index + lane/16)
+#pragma unroll
+  for (int u = 0; u < XU; ++u) buf16_to_lds(rx, slot + (wave * XU + u) * 1024, xoff[u], 256u * (uint32_t)Q);
+  // codes: instruction i = tile i / LB, KiB i % LB; wavefront w takes i = w, w + W, ...
+#pragma unroll
+  for (int v = 0; v < (2 * kXwPairs * LB + W - 1) / W; ++v) {
+    const int i = wave + W * v;
+    if (i < ntl * LB) {
+      const int t = i / LB, c = i - t * LB;
+      buf16_to_lds(rw, slot + XB + t * TB + c * 1024, (uint32_t)lane * 16u + 1024u * c,
+                   ((uint32_t)(t0 + t) * KQ + Q) * (uint32_t)TB);
+    }
+  }
+  // scales: 128 B per tile; lane l of wavefront w (w < 2) brings 16 B of tile 8w + l/8
+  // (lanes past the run repeat its last tile into bytes nothing reads)
+  if (wave < 2 && 8 * wave < ntl) {
+    const int t = min(8 * wave + (lane >> 3), ntl - 1);
+    buf16_to_lds(rd, slot + XB + 2 * kXwPairs * TB + wave * 1024,
+                 ((uint32_t)(t0 + t) * KQ + Q) * 128u + 16u * (lane & 7), 0u);
+  }
+}
+
+template <int FMT, int MT, int EPI = 0, typename TO = float, int W = 4>
+__global__ __launch_bounds__(64 * W) void qgemm_xw_kernel(const f16* __restrict__ x, int ldx,
+                                                     const uint8_t* __restrict__ wq, const uint16_t* __restrict__ wd,
+                                                     float* __restrict__ part, int M, int N, int K, int nq,
+                                                     TO* __restrict__ act = nullptr) {
+  static_assert(EPI == 0 || EPI == 1, "balanced large-m GEMM epilogues: partials or SwiGLU");
+  static_assert(!is_row_fmt(FMT), "block formats only");
+  static_assert((W == 4 || W == 8) && MT % W == 0, "4 or 8 wavefronts; the fifth pair's rows split over all");
+  constexpr int TB = kXwTileBytes<FMT>, LB = TB / 1024;
+  constexpr int XB = 16 * MT * 256, WB = 2 * kXwPairs * TB, SLOT = kXwSlot<FMT, MT>;
+  constexpr int XU = 4 * MT / W;   // KiB of a quad's activations each wavefront brings in
+  constexpr int RH = W / 4;        // wavefronts per pair (each on MT/RH row tiles)
+  constexpr int MTW = MT / RH;     // row tiles of a wavefront's own pair
+  constexpr int MT5 = MT / W;      // row tiles of the fifth pair per wavefront
+  __shared__ __align__(16) uint8_t slot_a[SLOT];
+  __shared__ __align__(16) uint8_t slot_b[SLOT];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63, li = lane & 15, lg = lane >> 4;
+  const int KQ = K / 128, NTILES = (N + 15) / 16, NP = (NTILES + 1) / 2;
+  const int p0 = (int)((long)blockIdx.x * NP / gridDim.x);
+  const int cnt = (int)((long)(blockIdx.x + 1) * NP / gridDim.x) - p0;  // 1..5 pairs (host-checked)
+  const int t0 = 2 * p0, ntl = min(2 * cnt, NTILES - t0);
+  const int split = blockIdx.y, q0 = split * nq, nqs = min(nq, KQ - q0);
+  const int m0 = blockIdx.z * 16 * MT;
+
+  const rsrc_t rx = make_rsrc(x, (uint32_t)((size_t)M * ldx * 2));
+  const uint32_t ntiles_total = (uint32_t)NTILES * KQ;
+  const rsrc_t rw = make_rsrc(wq, ntiles_total * (uint32_t)TB);
+  const rsrc_t rd = make_rsrc(wd, ntiles_total * 128u);
+  uint32_t xoff[XU];
+#pragma unroll
+  for (int u = 0; u < XU; ++u) {
+    const int r = 4 * (wave * XU + u) + (lane >> 4);
+    const int g = (lane & 15) ^ (r & 15);
+    xoff[u] = (uint32_t)min(m0 + r, M - 1) * (uint32_t)ldx * 2u + 16u * g;
+  }
+
+  const int pw = wave & 3, aw = (wave >> 2) * MTW;  // own pair of the run and its first row tile
+  const bool own = pw < cnt;
+  const bool fifth = cnt == kXwPairs;              // pair 4, rows wave*MT5 .. of it
+  f32x4 acc[MTW][2], acc5[MT5][2];
+#pragma unroll
+  for (int a = 0; a < MTW; ++a) acc[a][0] = acc[a][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int a = 0; a < MT5; ++a) acc5[a][0] = acc5[a][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+  int xo[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) xo[j] = li * 256 + (((4 * j + lg) ^ li) << 4);
+
+  // One tile pair (local tiles tl, tl+1) over row tiles a0 .. a0+NA-1 of the slot.
+  auto pair_mma = [&]<int NA>(const uint8_t* sl, int tl, int a0, f32x4 (&ac)[NA][2]) __attribute__((always_inline)) {
+    f16x8 wb[2][4];
+    float dj[2][4];
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      const uint8_t* codes = sl + XB + (tl + b) * TB + lane * 16 * LB;
+      const uint2 dd = *reinterpret_cast<const uint2*>(sl + XB + WB + (tl + b) * 128 + li * 8);
+      uint4 v[LB];
+#pragma unroll
+      for (int c = 0; c < LB; ++c) v[c] = *reinterpret_cast<const uint4*>(codes + 16 * c);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if constexpr (layout_fmt(FMT) == CIR_Q4_0) {
+          wb[b][j] = dq_q4((j == 0) ? v[0].x : (j == 1) ? v[0].y : (j == 2) ? v[0].z : v[0].w);
+        } else {
+          const uint4 vv = v[j >> 1];
+          wb[b][j] = dq_q8((j & 1) ? vv.z : vv.x, (j & 1) ? vv.w : vv.y);
+        }
+        const uint32_t dw = (j < 2) ? dd.x : dd.y;
+        dj[b][j] = static_cast<float>(__builtin_bit_cast(f16, (uint16_t)((j & 1) ? (dw >> 16) : (dw & 0xFFFFu))));
+      }
+    }
+#pragma unroll
+    for (int a = 0; a < NA; ++a) {
+      f16x8 xf[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) xf[j] = *reinterpret_cast<const f16x8*>(sl + (a0 + a) * 4096 + xo[j]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        f32x4 c[2];
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+          c[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xf[j], wb[b][j], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) ac[a][b][r] = fmaf(dj[b][j], c[b][r], ac[a][b][r]);
+      }
+    }
+  };
+  auto compute = [&](const uint8_t* sl) __attribute__((always_inline)) {
+    if (own) pair_mma.template operator()<MTW>(sl, 2 * pw, aw, acc);
+    if (fifth) pair_mma.template operator()<MT5>(sl, 2 * (kXwPairs - 1), wave * MT5, acc5);
+  };
+
+  // Quad i computes from slot i & 1 while quad i+1 comes into the other; the wait for
+  // that DMA and the barrier end the step.
+  xw_dma<FMT, MT, W>(slot_a, rx, rw, rd, xoff, wave, lane, t0, ntl, KQ, q0);
+  __syncthreads();
+  int i = 0;
+#pragma nounroll
+  for (; i + 2 <= nqs; i += 2) {
+    if (i + 1 < nqs) xw_dma<FMT, MT, W>(slot_b, rx, rw, rd, xoff, wave, lane, t0, ntl, KQ, q0 + i + 1);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(slot_a);
+    __syncthreads();
+    if (i + 2 < nqs) xw_dma<FMT, MT, W>(slot_a, rx, rw, rd, xoff, wave, lane, t0, ntl, KQ, q0 + i + 2);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(slot_b);
+    __syncthreads();
+  }
+  if (i < nqs) compute(slot_a);  // an odd count: the last quad sits in slot a
+  if constexpr (kAccScale<FMT> != 1.f) {
+#pragma unroll
+    for (int a = 0; a < MTW; ++a) acc[a][0] *= kAccScale<FMT>, acc[a][1] *= kAccScale<FMT>;
+#pragma unroll
+    for (int a = 0; a < MT5; ++a) acc5[a][0] *= kAccScale<FMT>, acc5[a][1] *= kAccScale<FMT>;
+  }
+
+  // Pair p of the run (tiles t0 + 2p, +1) over row tiles a0 .. a0+NA-1.
+  auto store = [&]<int NA>(int p, int a0, const f32x4 (&ac)[NA][2]) __attribute__((always_inline)) {
+    const int nt = t0 + 2 * p;
+    if constexpr (EPI == 1) {
+      const int inter = N / 2;
+      const int col = (nt >> 1) * 16 + li;
+      if (nt + 1 < NTILES && col < inter) {
+#pragma unroll
+        for (int a = 0; a < NA; ++a)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int m = m0 + 16 * (a0 + a) + 4 * lg + r;
+            const float g = ac[a][0][r], u = ac[a][1][r];
+            if (m < M) act[(size_t)m * inter + col] = static_cast<TO>(as_f32_value((g / (1.0f + expf(-g))) * u));
+          }
+      }
+    } else {
+#pragma unroll
+      for (int a = 0; a < NA; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+          const int n = (nt + b) * 16 + li;
+          if (nt + b < NTILES && n < N) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int m = m0 + 16 * (a0 + a) + 4 * lg + r;
+              if (m < M) part[((size_t)split * M + m) * N + n] = ac[a][b][r];
+            }
+          }
+        }
+    }
+  };
+  if (own) store.template operator()<MTW>(pw, aw, acc);
+  if (fifth) store.template operator()<MT5>(kXwPairs - 1, wave * MT5, acc5);
+}
+
 // m <= 8 (qgemv_kernel): a workgroup of W wavefronts owns W*NT row tiles, and each
 // wavefront streams its own NT tiles over the workgroup's k-range (grid.y splits k)
 // with no barrier inside the loop.  The m activation rows of that k-range are staged
@@ -1383,8 +1587,9 @@ void launch_qgemm_xs(const f16* x, int ldx, const uint8_t* wq, const uint16_t* w
 
 // Large m: activation rows per workgroup (16 * MT).
 constexpr int xl_mt(int m) { return m <= 64 ? 4 : 8; }
-// The SwiGLU launch (one split, so the column groups alone set the workgroup count)
-// keeps 64 rows per workgroup up to m = 128: at the Qwen2-7B gate|up (n 37888, 296
+// The large-m SwiGLU launch (one split, so the column groups alone set the workgroup
+// count; at 32 < m <= 128 it serves the row formats, which the balanced kernel does not
+// take) keeps 64 rows per workgroup up to m = 128: at the Qwen2-7B gate|up (n 37888, 296
 // column groups) 128 rows per workgroup leave 296 workgroups, a second round on 40 CUs,
 // while two 64-row blocks give 592 smaller ones at 3 wavefronts per SIMD (158 VGPRs
 // against 202): 83.2-86.0 us against 90.3-90.9 (Q8_0, m = 128, same box, alternated).
@@ -1458,6 +1663,32 @@ void launch_qgemm_xl_argmax(const f16* x, int ldx, const uint8_t* wq, const uint
   qgemm_xl_kernel<FMT, MT, DW, 2, float, W>
       <<<grid, 64 * W, 0, s>>>(x, ldx, wq, wd, cand_v, M, N, K, K / 128, reinterpret_cast<float*>(cand_i));
   argmax_cand_kernel<<<M, 256, 0, s>>>(cand_v, cand_i, (int)grid.x * W, M, ids);
+}
+
+// The balanced large-m kernel's workgroups: one per CU while the tile pairs allow
+// (1..5 pairs each), more only when the pairs exceed 5 per CU.
+int xw_workgroups(int n) {
+  const int np = ((n + 15) / 16 + 1) / 2;
+  const int need = (np + kXwPairs - 1) / kXwPairs;
+  const int one_round = np < kCUs ? np : kCUs;
+  return need > one_round ? need : one_round;
+}
+
+// The fused SwiGLU at 32 < m <= 128 (block formats) runs the balanced kernel, 4 wavefronts
+// (8, two per pair, measured no faster).  At the Qwen2-7B gate|up (Q8_0, 12 weight copies
+// rotated): m = 128 78.6-81.0 us against 81.4-85.5 for the large-m kernel in 64-row
+// blocks (64-row blocks of the balanced kernel: 84.9), m = 64 49.2-51.0 against 54.5-56.4.
+// The gain is less than the per-CU bytes suggest (1.5 MB against 2.8 MB on the busiest
+// CU): with one workgroup per CU the quads' DMA and compute alternate more than overlap.
+bool use_xw_swiglu(int m) { return m > 32 && m <= 128; }
+
+template <int FMT, int MT, int EPI, typename TO = float>
+void launch_qgemm_xw(const f16* x, int ldx, const uint8_t* wq, const uint16_t* wd, float* part, int M, int N, int K,
+                     int splits, hipStream_t s, TO* act = nullptr) {
+  constexpr int W = 4;
+  dim3 grid(xw_workgroups(N), splits, (M + 16 * MT - 1) / (16 * MT));
+  qgemm_xw_kernel<FMT, MT, EPI, TO, W>
+      <<<grid, 64 * W, 0, s>>>(x, ldx, wq, wd, part, M, N, K, (K / 128 + splits - 1) / splits, act);
 }
 
 // Workgroup rows: 4 wavefronts x NT tiles x 16.  m <= 16 takes NT = 1 (64 rows per
@@ -1636,6 +1867,17 @@ extern "C" int cir_qgemm_swiglu(const void* x, int ldx, const void* w_tiled, int
   const f16* xh = static_cast<const f16*>(x);
   hipStream_t s = as_stream(stream);
   auto go = [&]<int FMT>() {
+    if constexpr (!is_row_fmt(FMT)) {
+      if (use_xw_swiglu(m)) {
+        auto xw = [&]<int MT>() {
+          if (odt == CIR_F16) launch_qgemm_xw<FMT, MT, 1, f16>(xh, ldx, q, d, nullptr, m, n, k, 1, s, static_cast<f16*>(out));
+          else launch_qgemm_xw<FMT, MT, 1, float>(xh, ldx, q, d, nullptr, m, n, k, 1, s, static_cast<float*>(out));
+        };
+        if (m <= 64) xw.template operator()<4>();
+        else xw.template operator()<8>();
+        return;
+      }
+    }
     if (use_xl(m, n, k, false)) {
       auto xl = [&]<int MT>() {
         if (odt == CIR_F16) launch_qgemm_xl<FMT, MT, 1, f16>(xh, ldx, q, d, nullptr, m, n, k, 1, s, static_cast<f16*>(out));
@@ -1731,6 +1973,8 @@ extern "C" const char* cir_qgemm_plan(int op, int fmt, int m, int n, int k, int 
       if (!use_xl(m, n, k)) return "qgemm_xs_kernel<NT=2,MT=2>";
       return m <= 64 ? "qgemm_xl_kernel<MT=4>" : "qgemm_xl_kernel<MT=8>";
     case CIR_GEMM_SWIGLU:
+      if (!is_row_fmt(fmt) && use_xw_swiglu(m))
+        return m <= 64 ? "qgemm_xw_kernel<MT=4,EPI=swiglu>" : "qgemm_xw_kernel<MT=8,EPI=swiglu>";
       if (use_xl(m, n, k, false))
         return xl_mt_swiglu(m) == 4 ? "qgemm_xl_kernel<MT=4,EPI=swiglu>" : "qgemm_xl_kernel<MT=8,EPI=swiglu>";
       return m <= 16 ? "qgemm_xs_kernel<NT=2,MT=1,EPI=swiglu>" : "qgemm_xs_kernel<NT=2,MT=2,EPI=swiglu>";

@@ -537,9 +537,9 @@ def test_qgemm_swiglu_matches_gemm_then_epilogue(device, fmt, m, k):
     and within the fp16 bound of the fp64 oracle. At m <= 8 the reference side runs the GEMV (k = 4096 stages
     all of an 8-row activation in 64 KiB of LDS): with 32 quads or more the fused kernel sums two k-groups (even
     and odd quads) and then adds them, the GEMV sums the quads in order, so there the outputs agree to one fp16
-    ulp (the fp32 sums differ in rounding only); with fewer quads, bit for bit.  m = 100 and 128 run the large-m
-    SwiGLU in 64-row blocks against 128-row blocks for the partials (a partly filled last block at 100), m = 200 in
-    128-row blocks."""
+    ulp (the fp32 sums differ in rounding only); with fewer quads, bit for bit.  m = 48, 100 and 128 run the
+    balanced large-m SwiGLU (64- and 128-row blocks, a partly filled one at 100) against the large-m kernel's
+    partials, m = 200 the large-m SwiGLU in 128-row blocks."""
     from cacheir_amd import kernels
 
     rng = np.random.default_rng(11 + m + k)
@@ -566,6 +566,40 @@ def test_qgemm_swiglu_matches_gemm_then_epilogue(device, fmt, m, k):
     g64, u64 = xf @ dec(gate, k).astype(np.float64).T, xf @ dec(up, k).astype(np.float64).T
     want = g64 / (1.0 + np.exp(-g64)) * u64
     err = np.abs(got.double().cpu().numpy() - want) - (2e-3 + 1e-2 * np.abs(want))
+    assert np.all(err <= 0), err.max()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
+@pytest.mark.parametrize("m,inter", [(40, 17600), (128, 17600), (100, 5008), (128, 2304), (130, 17600)])
+def test_qgemm_swiglu_large_m_column_runs(device, fmt, m, inter):
+    """The fused SwiGLU at m > 32 over intermediate sizes that give each workgroup 4-5 gate/up pairs (17600: 1100
+    pairs over 256 workgroups), 1-2 pairs (5008) and one (2304), with 64- and 128-row blocks and a second, partly
+    filled row block at m = 130: bitwise equal to the partials of cir_qgemm (splits 1) + cir_epilogue_swiglu, and
+    within the fp16 bound of the fp64 oracle on a sample of columns."""
+    from cacheir_amd import kernels
+
+    rng = np.random.default_rng(m + inter)
+    k = 512
+    enc = quant.random_q4_0 if fmt == "q4_0" else quant.random_q8_0
+    dec = quant.decode_q4_0 if fmt == "q4_0" else quant.decode_q8_0
+    code = kernels.FMT_NAMES[fmt]
+    gate, up = enc(rng, inter, k)[0], enc(rng, inter, k)[0]
+    x = rng.standard_normal((m, k)).astype(np.float16)
+    xd = to_dev(x, device)
+    g_dev, u_dev = to_dev(gate, device), to_dev(up, device)
+    w_cat = kernels.QWeight.from_blocks(torch.cat([g_dev.reshape(-1), u_dev.reshape(-1)]), code, 2 * inter, k)
+    ref = kernels.epilogue_swiglu(kernels.qgemm_partial(xd, w_cat, splits=1), torch.float16)
+    w_il = kernels.QWeight.from_blocks(kernels.interleave_gate_up(g_dev, u_dev, inter).reshape(-1), code, 2 * inter, k)
+    got = kernels.qgemm_swiglu(xd, w_il, torch.float16)
+    torch.cuda.synchronize()
+    assert torch.equal(got, ref)
+    cols = np.unique(np.concatenate([np.arange(0, inter, 97), np.arange(inter - 40, inter)]))
+    xf = x.astype(np.float64)
+    g64 = xf @ dec(gate[cols], k).astype(np.float64).T
+    u64 = xf @ dec(up[cols], k).astype(np.float64).T
+    want = g64 / (1.0 + np.exp(-g64)) * u64
+    err = np.abs(got.double().cpu().numpy()[:, cols] - want) - (2e-3 + 1e-2 * np.abs(want))
     assert np.all(err <= 0), err.max()
 
 

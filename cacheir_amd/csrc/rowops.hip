@@ -136,8 +136,12 @@ __global__ __launch_bounds__(kEmbThreads) void embedding_kernel(const int64_t* _
 
 // Residual epilogue + RMSNorm of the result, one workgroup per row, 4 columns per
 // thread per step: h = residual + sum of partials (fp32, to h_out) and
-// xn = (h * rsqrt(mean(h^2) + eps)) * w.  N % 4 == 0 and N <= 8192.
-template <int SMAX, typename TW, typename TO>
+// xn = (h * rsqrt(mean(h^2) + eps)) * w.  N % 4 == 0 and N <= 8192; TWO (N > 4096)
+// gives each thread a second column group.  Its registers are compiled in only when the
+// host asks for it: with 16 splits they hold 2 x 16 float4 partials, 128 VGPRs, and
+// spill (a 9-split norm of 128 rows of 3584 took 10.2 us with them compiled in); rows
+// past 4096 with more than 8 splits still take that spilling variant.
+template <int SMAX, bool TWO, typename TW, typename TO>
 __global__ __launch_bounds__(kRowThreads) void residual_rmsnorm_kernel(
     const float* __restrict__ part, int splits, const float* __restrict__ resid, float* __restrict__ h_out,
     const TW* __restrict__ w, TO* __restrict__ xn, int M, int N, float eps) {
@@ -145,14 +149,14 @@ __global__ __launch_bounds__(kRowThreads) void residual_rmsnorm_kernel(
   const int r = blockIdx.x;
   const size_t plane = (size_t)M * N;
   // Every load of the thread (partials of both column groups, residual, norm weights) is
-  // issued before the first add, so the row costs one memory round trip; the second
-  // group exists only for rows longer than 4 * kRowThreads (uniform branch).
-  const bool second = N > 4 * kRowThreads;
-  float4 pv[2][SMAX], q[2], wv[2];
-  size_t idx[2];
-  bool ok[2];
+  // issued before the first add, so the row costs one memory round trip.
+  constexpr int G = TWO ? 2 : 1;
+  const bool second = TWO;
+  float4 pv[G][SMAX], q[G], wv[G];
+  size_t idx[G];
+  bool ok[G];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
+  for (int i = 0; i < G; ++i) {
     const int c = 4 * (threadIdx.x + i * kRowThreads);
     ok[i] = c < N;
     const int cc = ok[i] ? c : 0;
@@ -165,10 +169,10 @@ __global__ __launch_bounds__(kRowThreads) void residual_rmsnorm_kernel(
       wv[i] = load4(w + cc);
     }
   }
-  float4 v[2];
+  float4 v[G];
   float ss = 0.f;
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
+  for (int i = 0; i < G; ++i) {
     float4 t = {0.f, 0.f, 0.f, 0.f};
     if ((i == 0 || second) && ok[i]) {
       float4 p = pv[i][0];  // partials in split order, then the residual (as split_sum4 + add)
@@ -188,7 +192,7 @@ __global__ __launch_bounds__(kRowThreads) void residual_rmsnorm_kernel(
   }
   const float scale = 1.0f / sqrtf(block_sum_1024(ss, scratch) / (float)N + eps);
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
+  for (int i = 0; i < G; ++i) {
     if ((i == 0 || second) && ok[i])
       store4(xn + idx[i], make_float4((v[i].x * scale) * wv[i].x, (v[i].y * scale) * wv[i].y,
                                       (v[i].z * scale) * wv[i].z, (v[i].w * scale) * wv[i].w));
@@ -459,9 +463,15 @@ extern "C" int cir_epilogue_residual_rmsnorm(const float* y_partial, int splits,
   CIR_CHECK_ARG(y_partial && residual && h_out && norm_w && xn, "epilogue_residual_rmsnorm: null pointer");
   hipStream_t s = as_stream(stream);
   return with_smax(splits, [&]<int S>() {
-#define CIR_RR(TW, TO)                                                                                               \
-  residual_rmsnorm_kernel<S, TW, TO><<<m, kRowThreads, 0, s>>>(y_partial, splits, residual, h_out, (const TW*)norm_w, \
-                                                                (TO*)xn, m, n, eps)
+#define CIR_RR(TW, TO)                                                                                           \
+  do {                                                                                                           \
+    if (n > 4 * kRowThreads)                                                                                     \
+      residual_rmsnorm_kernel<S, true, TW, TO><<<m, kRowThreads, 0, s>>>(y_partial, splits, residual, h_out,     \
+                                                                         (const TW*)norm_w, (TO*)xn, m, n, eps); \
+    else                                                                                                         \
+      residual_rmsnorm_kernel<S, false, TW, TO><<<m, kRowThreads, 0, s>>>(y_partial, splits, residual, h_out,    \
+                                                                          (const TW*)norm_w, (TO*)xn, m, n, eps); \
+  } while (0)
     if (wdt == CIR_F32 && xdt == CIR_F32) CIR_RR(float, float);
     else if (wdt == CIR_F32 && xdt == CIR_F16) CIR_RR(float, f16);
     else if (wdt == CIR_F16 && xdt == CIR_F32) CIR_RR(f16, float);

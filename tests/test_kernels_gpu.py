@@ -739,6 +739,36 @@ def test_row_packed_dequant_bit_exact_and_gemm(device, bits):
     assert np.all(np.abs(y2 - ref2) - (2e-3 + 1e-2 * np.abs(ref2)) <= 0)
 
 
+@pytest.mark.parametrize("splits", [1, 3, 8, 9, 16])
+@pytest.mark.parametrize("n", [256, 3584, 4096, 5120])
+def test_residual_rmsnorm_epilogue(device, splits, n):
+    """cir_epilogue_residual_rmsnorm: h = residual + the split partials summed in split order (fp32, bit for bit
+    against the same order in numpy), xn = RMSNorm(h) * w against the oracle, fp32 and fp16 outputs.  Covers 1-16
+    splits (the 16-split variant serves the 9 of the large-m down projection) and rows past 4096 (a second column
+    group per thread)."""
+    from cacheir_amd import kernels
+
+    rng = np.random.default_rng(splits * 10000 + n)
+    m = 5
+    part = rng.standard_normal((splits, m, n)).astype(np.float32)
+    resid = rng.standard_normal((m, n)).astype(np.float32)
+    w = rng.standard_normal(n).astype(np.float16)
+    p = part[0].copy()
+    for s_ in range(1, splits):
+        p = p + part[s_]
+    h_want = resid + p
+    for odt in (torch.float32, torch.float16):
+        h = torch.empty((m, n), device=device, dtype=torch.float32)
+        xn = torch.empty((m, n), device=device, dtype=odt)
+        kernels.epilogue_residual_rmsnorm(to_dev(part, device), to_dev(resid, device), to_dev(w, device), 1e-5, h, xn)
+        assert np.array_equal(h.cpu().numpy().view(np.uint32), h_want.view(np.uint32))
+        want = ops.rms_norm(h_want, w.astype(np.float32), 1e-5)
+        if odt == torch.float32:
+            np.testing.assert_allclose(xn.cpu().numpy(), want, rtol=1e-5, atol=1e-5)
+        else:
+            close16(xn.float().cpu().numpy(), want)
+
+
 def test_row_kernels(device):
     from cacheir_amd import kernels
 

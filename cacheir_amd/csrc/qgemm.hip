@@ -1699,6 +1699,8 @@ constexpr int xs_rows_per_group(int m) { return m <= 16 ? 64 : 128; }
 
 // k-split: the smallest power of two that gives >= 192 workgroups, keeping at least
 // 4 quads per split (split-k partials cost 4*m*n bytes each, so no more than needed).
+// The threshold, swept on the config-4 step at m = 32 (same box, two passes each):
+// 96 / 128 / 192 / 256 / 384 gave 3.80 / 3.69 / 3.45-3.54 / 3.58 / 3.70 ms.
 int default_splits(int m, int n, int k) {
   if (m <= 8) {
     if (const int s = gemv_splits(m, n, k)) return s;

@@ -881,9 +881,9 @@ __global__ __launch_bounds__(64 * W) void qgemm_xl_kernel(const f16* __restrict_
 // Wavefront w computes pair w over all rows and, in a 5-pair run, rows w*MT/4.. of the
 // fifth pair: each dequantized fragment feeds MT (or MT/4) MFMAs, and the four
 // wavefronts have the same MFMA count.  Per tile, quad and block the arithmetic is the
-// large-m kernel's in the same order, so for the same split both give the same bits.
-// EPI 0: fp32 partials part[split][m][n]; EPI 1: SwiGLU over interleaved gate/up tiles
-// (one split), out[m][N/2] in type TO.  Block formats only.
+// large-m kernel's in the same order, so both give the same bits over one split.  The
+// epilogue is the SwiGLU over interleaved gate/up tiles, out[m][N/2] in type TO (one
+// split, the whole of k).  Block formats only.
 constexpr int kXwPairs = 5;
 template <int FMT>
 inline constexpr int kXwTileBytes = 1024 * Stage<FMT, 1, 1>::LB;  // codes of one tile and quad
@@ -920,19 +920,17 @@ __device__ __forceinline__ void xw_dma(uint8_t* slot, rsrc_t rx, rsrc_t rw, rsrc
   }
 }
 
-template <int FMT, int MT, int EPI = 0, typename TO = float, int W = 4>
-__global__ __launch_bounds__(64 * W) void qgemm_xw_kernel(const f16* __restrict__ x, int ldx,
+constexpr int kXwWaves = 4;
+template <int FMT, int MT, typename TO>
+__global__ __launch_bounds__(64 * kXwWaves) void qgemm_xw_kernel(const f16* __restrict__ x, int ldx,
                                                      const uint8_t* __restrict__ wq, const uint16_t* __restrict__ wd,
-                                                     float* __restrict__ part, int M, int N, int K, int nq,
-                                                     TO* __restrict__ act = nullptr) {
-  static_assert(EPI == 0 || EPI == 1, "balanced large-m GEMM epilogues: partials or SwiGLU");
+                                                     int M, int N, int K, TO* __restrict__ act) {
   static_assert(!is_row_fmt(FMT), "block formats only");
-  static_assert((W == 4 || W == 8) && MT % W == 0, "4 or 8 wavefronts; the fifth pair's rows split over all");
+  constexpr int W = kXwWaves;
+  static_assert(MT % W == 0, "the fifth pair's rows split over the wavefronts");
   constexpr int TB = kXwTileBytes<FMT>, LB = TB / 1024;
   constexpr int XB = 16 * MT * 256, WB = 2 * kXwPairs * TB, SLOT = kXwSlot<FMT, MT>;
   constexpr int XU = 4 * MT / W;   // KiB of a quad's activations each wavefront brings in
-  constexpr int RH = W / 4;        // wavefronts per pair (each on MT/RH row tiles)
-  constexpr int MTW = MT / RH;     // row tiles of a wavefront's own pair
   constexpr int MT5 = MT / W;      // row tiles of the fifth pair per wavefront
   __shared__ __align__(16) uint8_t slot_a[SLOT];
   __shared__ __align__(16) uint8_t slot_b[SLOT];
@@ -942,7 +940,7 @@ __global__ __launch_bounds__(64 * W) void qgemm_xw_kernel(const f16* __restrict_
   const int p0 = (int)((long)blockIdx.x * NP / gridDim.x);
   const int cnt = (int)((long)(blockIdx.x + 1) * NP / gridDim.x) - p0;  // 1..5 pairs (host-checked)
   const int t0 = 2 * p0, ntl = min(2 * cnt, NTILES - t0);
-  const int split = blockIdx.y, q0 = split * nq, nqs = min(nq, KQ - q0);
+  const int q0 = 0, nqs = KQ;
   const int m0 = blockIdx.z * 16 * MT;
 
   const rsrc_t rx = make_rsrc(x, (uint32_t)((size_t)M * ldx * 2));
@@ -957,12 +955,11 @@ __global__ __launch_bounds__(64 * W) void qgemm_xw_kernel(const f16* __restrict_
     xoff[u] = (uint32_t)min(m0 + r, M - 1) * (uint32_t)ldx * 2u + 16u * g;
   }
 
-  const int pw = wave & 3, aw = (wave >> 2) * MTW;  // own pair of the run and its first row tile
-  const bool own = pw < cnt;
-  const bool fifth = cnt == kXwPairs;              // pair 4, rows wave*MT5 .. of it
-  f32x4 acc[MTW][2], acc5[MT5][2];
+  const bool own = wave < cnt;          // pair `wave` of the run, all rows
+  const bool fifth = cnt == kXwPairs;    // pair 4, row tiles wave*MT5 .. of it
+  f32x4 acc[MT][2], acc5[MT5][2];
 #pragma unroll
-  for (int a = 0; a < MTW; ++a) acc[a][0] = acc[a][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int a = 0; a < MT; ++a) acc[a][0] = acc[a][1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int a = 0; a < MT5; ++a) acc5[a][0] = acc5[a][1] = f32x4{0.f, 0.f, 0.f, 0.f};
   int xo[4];
@@ -1011,7 +1008,7 @@ __global__ __launch_bounds__(64 * W) void qgemm_xw_kernel(const f16* __restrict_
     }
   };
   auto compute = [&](const uint8_t* sl) __attribute__((always_inline)) {
-    if (own) pair_mma.template operator()<MTW>(sl, 2 * pw, aw, acc);
+    if (own) pair_mma.template operator()<MT>(sl, 2 * wave, 0, acc);
     if (fifth) pair_mma.template operator()<MT5>(sl, 2 * (kXwPairs - 1), wave * MT5, acc5);
   };
 
@@ -1034,44 +1031,28 @@ __global__ __launch_bounds__(64 * W) void qgemm_xw_kernel(const f16* __restrict_
   if (i < nqs) compute(slot_a);  // an odd count: the last quad sits in slot a
   if constexpr (kAccScale<FMT> != 1.f) {
 #pragma unroll
-    for (int a = 0; a < MTW; ++a) acc[a][0] *= kAccScale<FMT>, acc[a][1] *= kAccScale<FMT>;
+    for (int a = 0; a < MT; ++a) acc[a][0] *= kAccScale<FMT>, acc[a][1] *= kAccScale<FMT>;
 #pragma unroll
     for (int a = 0; a < MT5; ++a) acc5[a][0] *= kAccScale<FMT>, acc5[a][1] *= kAccScale<FMT>;
   }
 
-  // Pair p of the run (tiles t0 + 2p, +1) over row tiles a0 .. a0+NA-1.
+  // SwiGLU of pair p of the run (gate tile t0 + 2p, up tile t0 + 2p + 1) over row tiles a0 .. a0+NA-1.
   auto store = [&]<int NA>(int p, int a0, const f32x4 (&ac)[NA][2]) __attribute__((always_inline)) {
     const int nt = t0 + 2 * p;
-    if constexpr (EPI == 1) {
-      const int inter = N / 2;
-      const int col = (nt >> 1) * 16 + li;
-      if (nt + 1 < NTILES && col < inter) {
-#pragma unroll
-        for (int a = 0; a < NA; ++a)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int m = m0 + 16 * (a0 + a) + 4 * lg + r;
-            const float g = ac[a][0][r], u = ac[a][1][r];
-            if (m < M) act[(size_t)m * inter + col] = static_cast<TO>(as_f32_value((g / (1.0f + expf(-g))) * u));
-          }
-      }
-    } else {
+    const int inter = N / 2;
+    const int col = (nt >> 1) * 16 + li;
+    if (nt + 1 < NTILES && col < inter) {
 #pragma unroll
       for (int a = 0; a < NA; ++a)
 #pragma unroll
-        for (int b = 0; b < 2; ++b) {
-          const int n = (nt + b) * 16 + li;
-          if (nt + b < NTILES && n < N) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const int m = m0 + 16 * (a0 + a) + 4 * lg + r;
-              if (m < M) part[((size_t)split * M + m) * N + n] = ac[a][b][r];
-            }
-          }
+        for (int r = 0; r < 4; ++r) {
+          const int m = m0 + 16 * (a0 + a) + 4 * lg + r;
+          const float g = ac[a][0][r], u = ac[a][1][r];
+          if (m < M) act[(size_t)m * inter + col] = static_cast<TO>(as_f32_value((g / (1.0f + expf(-g))) * u));
         }
     }
   };
-  if (own) store.template operator()<MTW>(pw, aw, acc);
+  if (own) store.template operator()<MT>(wave, 0, acc);
   if (fifth) store.template operator()<MT5>(kXwPairs - 1, wave * MT5, acc5);
 }
 
@@ -1682,13 +1663,11 @@ int xw_workgroups(int n) {
 // CU): with one workgroup per CU the quads' DMA and compute alternate more than overlap.
 bool use_xw_swiglu(int m) { return m > 32 && m <= 128; }
 
-template <int FMT, int MT, int EPI, typename TO = float>
-void launch_qgemm_xw(const f16* x, int ldx, const uint8_t* wq, const uint16_t* wd, float* part, int M, int N, int K,
-                     int splits, hipStream_t s, TO* act = nullptr) {
-  constexpr int W = 4;
-  dim3 grid(xw_workgroups(N), splits, (M + 16 * MT - 1) / (16 * MT));
-  qgemm_xw_kernel<FMT, MT, EPI, TO, W>
-      <<<grid, 64 * W, 0, s>>>(x, ldx, wq, wd, part, M, N, K, (K / 128 + splits - 1) / splits, act);
+template <int FMT, int MT, typename TO>
+void launch_qgemm_xw_swiglu(const f16* x, int ldx, const uint8_t* wq, const uint16_t* wd, TO* act, int M, int N, int K,
+                            hipStream_t s) {
+  dim3 grid(xw_workgroups(N), 1, (M + 16 * MT - 1) / (16 * MT));
+  qgemm_xw_kernel<FMT, MT, TO><<<grid, 64 * kXwWaves, 0, s>>>(x, ldx, wq, wd, M, N, K, act);
 }
 
 // Workgroup rows: 4 wavefronts x NT tiles x 16.  m <= 16 takes NT = 1 (64 rows per
@@ -1872,8 +1851,8 @@ extern "C" int cir_qgemm_swiglu(const void* x, int ldx, const void* w_tiled, int
     if constexpr (!is_row_fmt(FMT)) {
       if (use_xw_swiglu(m)) {
         auto xw = [&]<int MT>() {
-          if (odt == CIR_F16) launch_qgemm_xw<FMT, MT, 1, f16>(xh, ldx, q, d, nullptr, m, n, k, 1, s, static_cast<f16*>(out));
-          else launch_qgemm_xw<FMT, MT, 1, float>(xh, ldx, q, d, nullptr, m, n, k, 1, s, static_cast<float*>(out));
+          if (odt == CIR_F16) launch_qgemm_xw_swiglu<FMT, MT, f16>(xh, ldx, q, d, static_cast<f16*>(out), m, n, k, s);
+          else launch_qgemm_xw_swiglu<FMT, MT, float>(xh, ldx, q, d, static_cast<float*>(out), m, n, k, s);
         };
         if (m <= 64) xw.template operator()<4>();
         else xw.template operator()<8>();

@@ -878,9 +878,9 @@ __global__ __launch_bounds__(64 * W) void qgemm_xl_kernel(const f16* __restrict_
 // groups leave 2 or 3 workgroups per CU).  Per quad the weight codes and scales of the
 // run and the activations all go to LDS by buffer DMA, double-buffered in two separate
 // arrays so the compiler lets the LDS reads of one slot overlap the DMA into the other.
-// Wavefront w computes pair w over all rows and, in a 5-pair run, rows w*MT/4.. of the
-// fifth pair: each dequantized fragment feeds MT (or MT/4) MFMAs, and the four
-// wavefronts have the same MFMA count.  Per tile, quad and block the arithmetic is the
+// Wavefront w computes pair w over all rows and, in a 5-pair run, row tiles w*MT/4 ..
+// (w+1)*MT/4 - 1 of the fifth pair: each dequantized fragment feeds MT (or MT/4) MFMAs,
+// and in 4- and 5-pair runs the four wavefronts have the same MFMA count.  Per tile, quad and block the arithmetic is the
 // large-m kernel's in the same order, so both give the same bits over one split.  The
 // epilogue is the SwiGLU over interleaved gate/up tiles, out[m][N/2] in type TO (one
 // split, the whole of k).  Block formats only.

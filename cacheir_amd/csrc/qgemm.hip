@@ -651,7 +651,8 @@ __global__ __launch_bounds__(64 * W) void qgemm_xl_kernel(const f16* __restrict_
   constexpr int NT = 2;
   constexpr int LB = Stage<FMT, NT, 1>::LB;
   constexpr int kSlot = 16 * MT * 256;  // bytes of one quad of activations
-  __shared__ __align__(16) uint8_t smem[2 * kSlot];
+  __shared__ __align__(16) uint8_t smem0[kSlot];  // two arrays, not one: the compiler then
+  __shared__ __align__(16) uint8_t smem1[kSlot];  // lets reads of one run while DMA fills the other
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63, li = lane & 15, lg = lane >> 4;
   const int KQ = K / 128, NTILES = (N + 15) / 16;
@@ -675,9 +676,10 @@ __global__ __launch_bounds__(64 * W) void qgemm_xl_kernel(const f16* __restrict_
     xoff[u] = (uint32_t)min(m0 + r, M - 1) * (uint32_t)ldx * 2u + 16u * g;
   }
   auto dma_x = [&](int slot, int Q) __attribute__((always_inline)) {
+    uint8_t* sm = slot ? smem1 : smem0;
 #pragma unroll
     for (int u = 0; u < XU; ++u)
-      buf16_to_lds(rx, smem + slot * kSlot + (wave * XU + u) * 1024, xoff[u], 256u * (uint32_t)(q0 + Q));
+      buf16_to_lds(rx, sm + (wave * XU + u) * 1024, xoff[u], 256u * (uint32_t)(q0 + Q));
   };
 
   const uint32_t ntiles_total = (uint32_t)NTILES * KQ;
@@ -738,7 +740,7 @@ __global__ __launch_bounds__(64 * W) void qgemm_xl_kernel(const f16* __restrict_
           dj[b][j] = static_cast<float>(__builtin_bit_cast(f16, (uint16_t)((j & 1) ? (dw >> 16) : (dw & 0xFFFFu))));
         }
       }
-    const uint8_t* xq = smem + xslot * kSlot;
+    const uint8_t* xq = xslot ? smem1 : smem0;
 #pragma unroll
     for (int a = 0; a < MT; ++a) {
       f16x8 xf[4];
@@ -776,14 +778,29 @@ __global__ __launch_bounds__(64 * W) void qgemm_xl_kernel(const f16* __restrict_
   // the two slots apart) would wait for it, and for every load issued after it.  The
   // wait before the barrier covers the DMA but not the weights issued after it.
   int i = 0;
+  if constexpr (R % 2 == 0) {
+    // An even ring length keeps i even, so each step's slot S & 1 is known at compile time
+    // and the DMA can go out first: the compute reads the other array, which the compiler
+    // does not wait on.
 #pragma nounroll
-  for (; i + R <= nqs; i += R) {
-    each.template operator()<R>([&]<int S>() {
-      compute(ws[S], (i + S) & 1);
-      dma_x((i + S + 1) & 1, min(i + S + 1, nqs - 1));
-      issue((S + DW) % R, i + S + DW);
-      barrier();
-    });
+    for (; i + R <= nqs; i += R) {
+      each.template operator()<R>([&]<int S>() {
+        dma_x((S + 1) & 1, min(i + S + 1, nqs - 1));
+        compute(ws[S], S & 1);
+        issue((S + DW) % R, i + S + DW);
+        barrier();
+      });
+    }
+  } else {
+#pragma nounroll
+    for (; i + R <= nqs; i += R) {
+      each.template operator()<R>([&]<int S>() {
+        compute(ws[S], (i + S) & 1);
+        dma_x((i + S + 1) & 1, min(i + S + 1, nqs - 1));
+        issue((S + DW) % R, i + S + DW);
+        barrier();
+      });
+    }
   }
   each.template operator()<DW>([&]<int S>() {  // at most DW quads are left, in ring slots 0 .. DW-1
     if (i + S < nqs) {

@@ -772,40 +772,29 @@ __global__ __launch_bounds__(64 * W) void qgemm_xl_kernel(const f16* __restrict_
   dma_x(0, 0);
   each.template operator()<DW>([&]<int S>() { issue(S, S); });
   barrier();  // (the compiler waits for this wavefront's DMA before the barrier)
-  // Stage i: compute quad i, then DMA quad i+1 into the other slot and refill the ring,
-  // then the barrier that publishes quad i+1 (and frees slot i & 1).  The DMA goes out
-  // after the compute's LDS reads: issued before them, the compiler (which cannot tell
-  // the two slots apart) would wait for it, and for every load issued after it.  The
-  // wait before the barrier covers the DMA but not the weights issued after it.
+  // Stage i: DMA quad i+1 into the other slot, compute quad i, refill the ring, then the
+  // barrier that publishes quad i+1 (and frees slot i & 1).  The wait before the barrier
+  // covers the DMA and the loads issued before it, not the weights issued after it.
+  // An even ring length keeps i even, so each step's slot S & 1 is known at compile time
+  // and the DMA can go out first: the compute reads the other array, which the compiler
+  // does not wait on.  (With one array, or a slot known only at run time, it waits for
+  // the DMA and every load before it; an odd ring would need 2R steps unrolled, which
+  // spilled.)
+  static_assert(R % 2 == 0, "the slot of each step is fixed only for an even ring");
   int i = 0;
-  if constexpr (R % 2 == 0) {
-    // An even ring length keeps i even, so each step's slot S & 1 is known at compile time
-    // and the DMA can go out first: the compute reads the other array, which the compiler
-    // does not wait on.
 #pragma nounroll
-    for (; i + R <= nqs; i += R) {
-      each.template operator()<R>([&]<int S>() {
-        dma_x((S + 1) & 1, min(i + S + 1, nqs - 1));
-        compute(ws[S], S & 1);
-        issue((S + DW) % R, i + S + DW);
-        barrier();
-      });
-    }
-  } else {
-#pragma nounroll
-    for (; i + R <= nqs; i += R) {
-      each.template operator()<R>([&]<int S>() {
-        compute(ws[S], (i + S) & 1);
-        dma_x((i + S + 1) & 1, min(i + S + 1, nqs - 1));
-        issue((S + DW) % R, i + S + DW);
-        barrier();
-      });
-    }
+  for (; i + R <= nqs; i += R) {
+    each.template operator()<R>([&]<int S>() {
+      dma_x((S + 1) & 1, min(i + S + 1, nqs - 1));
+      compute(ws[S], S & 1);
+      issue((S + DW) % R, i + S + DW);
+      barrier();
+    });
   }
-  each.template operator()<DW>([&]<int S>() {  // at most DW quads are left, in ring slots 0 .. DW-1
+  each.template operator()<DW>([&]<int S>() {  // at most DW quads are left, in ring slots 0 .. DW-1 (i even)
     if (i + S < nqs) {
-      compute(ws[S], (i + S) & 1);
-      dma_x((i + S + 1) & 1, min(i + S + 1, nqs - 1));
+      if (i + S + 1 < nqs) dma_x((S + 1) & 1, i + S + 1);
+      compute(ws[S], S & 1);
       barrier();
     }
   });
@@ -1637,7 +1626,11 @@ bool splits_ok(int m, int n, int k, int splits) {
 template <int FMT, int MT, int EPI, typename TO = float>
 void launch_qgemm_xl(const f16* x, int ldx, const uint8_t* wq, const uint16_t* wd, float* part, int M, int N, int K,
                      int splits, hipStream_t s, TO* act = nullptr) {
-  constexpr int DW = layout_fmt(FMT) == CIR_Q4_0 ? 4 : 3;
+  // Ring of DW + 1 = 4 weight stages for both widths: an even ring lets the activation
+  // DMA go out before the compute (the kernel's even-ring path).  Q4_0 at m = 2048 (a
+  // 2048-token prefill): down 301-303 -> 289.9-290.3 us, QKV 147.8-148.2 -> 138.9-140.0
+  // against a 5-stage ring, prefill 46.7-46.8 -> 44.2 ms (6 stages: 44.4-44.7).
+  constexpr int DW = 3;
   constexpr int W = CIR_XL_W;
   const int NTILES = (N + 15) / 16;
   dim3 grid((NTILES + 2 * W - 1) / (2 * W), splits, (M + 16 * MT - 1) / (16 * MT));
@@ -1653,7 +1646,7 @@ void launch_qgemm_xl(const f16* x, int ldx, const uint8_t* wq, const uint16_t* w
 template <int FMT, int MT>
 void launch_qgemm_xl_argmax(const f16* x, int ldx, const uint8_t* wq, const uint16_t* wd, float* cand_v, int* cand_i,
                             int64_t* ids, int M, int N, int K, hipStream_t s) {
-  constexpr int DW = layout_fmt(FMT) == CIR_Q4_0 ? 4 : 3;
+  constexpr int DW = 3;  // as in launch_qgemm_xl
   constexpr int W = CIR_XL_W;
   static_assert(2 * 16 * W == 128, "argmax_cand_count assumes 128 columns per workgroup");
   const int NTILES = (N + 15) / 16;

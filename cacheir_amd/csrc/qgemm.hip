@@ -1459,9 +1459,11 @@ bool gemv_head_fits(int fmt, int m, int k) { return !is_row_fmt(fmt) && gemv_fit
 // 32 quads or more and the launch has at most one workgroup per CU, at any m
 // (measured: the unsplit gate|up + SwiGLU at k = 4096, 224 workgroups, gains ~4% at
 // m = 32 and ~10% at m = 1; the lm_head's 1002 workgroups lose 15%, and splits of
-// 4-14 quads lose with half as many per group).  Every epilogue of this kernel
-// (partials, SwiGLU, argmax) picks the same value for the same m, n and k, so their
-// sums run in the same order.
+// 4-14 quads lose with half as many per group).  The count depends on the launch's
+// workgroup count, which differs between epilogues: at m <= 16 the partials launch
+// (NT = 1) can have twice the workgroups of the SwiGLU launch (NT = 2) and take one
+// group where the SwiGLU takes two, so there the two sum the quads in different orders
+// and agree to rounding, not bit for bit.
 int xs_kgroups(int m, int quads, long workgroups) {
   int kg = (quads >= 32 && workgroups <= kCUs) ? 2 : (m > 16 ? CIR_XS_KG : 1);
   while (kg > 1 && quads % kg) kg /= 2;
@@ -1604,11 +1606,17 @@ bool use_xl(int m, int n, int k, bool splittable = true) {
 // Its k-split: as many splits as keep the launch at one round of workgroups over the
 // 256 CUs (down at m = 128: 9 splits, 252 workgroups: 42.3 us against 46.5 at 8 and 43.9
 // at 10), each split at least 4 quads.  The splits need not divide k/128: split s covers
-// quads s * ceil(kq / S) onward, the last one fewer.
+// quads s * ceil(kq / S) onward, the last one fewer.  The count is then lowered to
+// ceil(kq / len) for that split length len, so the last split is never empty (86 quads
+// at 16 splits would leave split 15 starting past the end; 15 splits of 6 quads do not).
 int xl_splits(int m, int n, int k) {
-  const long by_cus = 256 / xl_groups(m, n), by_len = (k / 128) / 4;
-  const long s = by_cus < by_len ? by_cus : by_len;
-  return s > 1 ? (int)s : 1;
+  const long kq = k / 128;
+  const long by_cus = 256 / xl_groups(m, n), by_len = kq / 4;
+  long s = by_cus < by_len ? by_cus : by_len;
+  if (s <= 1) return 1;
+  const long len = (kq + s - 1) / s;
+  s = (kq + len - 1) / len;
+  return (int)s;
 }
 
 // The k-splits a cir_qgemm launch accepts: those dividing k/128, and on the large-m

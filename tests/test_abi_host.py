@@ -79,6 +79,27 @@ def test_gemm_planner_splits_and_kernels_without_a_gpu():
     assert kernels.gemm_plan(P, q4, 32, 4096, 14336, 9) == "invalid"
 
 
+@pytest.mark.skipif(not hip.library_path().exists(), reason="libcacheir_hip.so not built")
+def test_default_splits_are_always_accepted():
+    """Whatever k-split the library proposes for a shape, its own launch accepts (no empty last split): the
+    Qwen2.5-3B down (n 2048, k 11008: 86 quads) at m = 64 once got 16 splits, which start split 15 past the end."""
+    from cacheir_amd import kernels
+
+    ns = (128, 896, 1536, 2048, 3584, 4096, 4608, 8960, 11008, 14336, 18944, 37888)
+    ks = (128, 512, 896 // 128 * 128, 1536, 2048, 3584, 8960, 11008, 14336, 18944)
+    bad = []
+    for fmt in (hip.CIR_Q4_0, hip.CIR_Q8_0):
+        for m in (1, 8, 16, 32, 33, 48, 64, 65, 96, 128, 200, 512):
+            for n in ns:
+                for k in ks:
+                    s = kernels.choose_splits(m, n, k)
+                    if kernels.gemm_plan(hip.GEMM_PARTIALS, fmt, m, n, k, s) == "invalid":
+                        bad.append((fmt, m, n, k, s))
+    assert not bad, bad[:10]
+    assert kernels.choose_splits(64, 2048, 11008) == 15  # 15 splits of 6 quads, the last 2
+    assert kernels.gemm_plan(hip.GEMM_PARTIALS, hip.CIR_Q8_0, 64, 2048, 11008, 15) != "invalid"
+
+
 def llama(layers=3, **kw):
     base = dict(architecture="LlamaForCausalLM", hidden_size=256, intermediate_size=512, num_layers=layers,
                 num_attention_heads=8, num_key_value_heads=2, vocab_size=1000, rope_theta=10000.0, rms_norm_eps=1e-5,

@@ -545,7 +545,8 @@ class HipRuntime:
                  weights: HipWeightStore | None = None, source=None, tokenizer=None,
                  prefix_cache: PrefixCache | None = None, kv_allocator: HipKVPageAllocator | None = None,
                  kv_capacity_pages: int = 64, memory_limit_mb: float | None = None, use_graphs: bool = True,
-                 _plans: dict | None = None, _inv_freq: dict | None = None, _gemm_plans: OrderedDict | None = None):
+                 max_plans: int = 16, _plans: OrderedDict | None = None, _inv_freq: dict | None = None,
+                 _gemm_plans: OrderedDict | None = None):
         if not torch.cuda.is_available():
             raise RuntimeError("HipRuntime requested a GPU, but torch.cuda.is_available() is false")
         hip.load()  # no CPU fallback: fail here if the kernel library is missing
@@ -577,7 +578,11 @@ class HipRuntime:
         self.prefix_cache = prefix_cache or PrefixCache(capacity=8)
         self.memory_limit_mb = memory_limit_mb
         self.use_graphs = bool(use_graphs)
-        self._plans: dict = _plans if _plans is not None else {}
+        # step plans, least recently used first; at most max_plans are kept (each owns its static buffers and up
+        # to two captured graphs), shared with every fork
+        self.max_plans = max(1, int(max_plans))
+        self._plans: OrderedDict = _plans if _plans is not None else OrderedDict()
+        self.plan_evictions = 0
         self._inv_freq: dict = _inv_freq if _inv_freq is not None else {}
         self.kernel_counts: OrderedDict[str, int] = OrderedDict()
         self.gemm_plans: OrderedDict[str, str] = _gemm_plans if _gemm_plans is not None else OrderedDict()
@@ -619,11 +624,20 @@ class HipRuntime:
         return self._inv_freq[key]
 
     def plan(self, mode: str, batch: int, q_len: int, max_pages: int) -> StepPlan:
+        """The step plan for this shape, built on first use (or after the pool was re-based).  The cache keeps the
+        ``max_plans`` most recently used plans: a scheduler whose batch size changes every round would otherwise
+        accumulate one plan, its buffers and its graphs per shape it ever ran."""
         key = (mode, batch, q_len, max_pages)
         plan = self._plans.get(key)
         if plan is None or plan.generation != self.kv_allocator.generation:
+            self._plans.pop(key, None)
+            while len(self._plans) >= self.max_plans:
+                self._plans.popitem(last=False)
+                self.plan_evictions += 1
             plan = StepPlan(self, mode, batch, q_len, max_pages)
             self._plans[key] = plan
+        else:
+            self._plans.move_to_end(key)
         return plan
 
     @staticmethod
@@ -679,7 +693,8 @@ class HipRuntime:
         """New session sharing artifact, weights, tokenizer, prefix cache, plans and the KV allocator."""
         return HipRuntime(self.artifact, device=str(self.device), dtype=self._dtype_name(), weights=self.weights,
                           tokenizer=self.tokenizer, prefix_cache=self.prefix_cache, kv_allocator=self.kv_allocator,
-                          memory_limit_mb=self.memory_limit_mb, use_graphs=self.use_graphs, _plans=self._plans,
+                          memory_limit_mb=self.memory_limit_mb, use_graphs=self.use_graphs,
+                          max_plans=self.max_plans, _plans=self._plans,
                           _inv_freq=self._inv_freq, _gemm_plans=self.gemm_plans)
 
     def _dtype_name(self) -> str:
@@ -790,12 +805,59 @@ class HipRuntime:
         for s in sessions:
             s._clear_rows()
         self._count("cacheir.rocm_prefill_batch_graph")
+        caches = [s.kv_cache for s in sessions]
         if len(set(lens)) == 1:
-            return self._execute([s.kv_cache for s in sessions], np.array(token_id_batches, dtype=np.int64),
-                                 "prefill")
-        out = torch.zeros((len(sessions), max(lens), self.config.vocab_size), dtype=torch.float32, device=self.device)
-        for b, (s, toks) in enumerate(zip(sessions, token_id_batches)):
-            out[b, : len(toks)] = s._execute([s.kv_cache], np.array([toks], dtype=np.int64), "prefill")[0]
+            return self._execute(caches, np.array(token_id_batches, dtype=np.int64), "prefill")
+        return self._prefill_padded(caches, token_id_batches)
+
+    def _prefill_padded(self, caches: list[HipPagedKVCache], batches: list[list[int]]) -> torch.Tensor:
+        """A variable-length prefill as one pass over the batch padded to the longest prompt (the reference pads
+        too, ``cuda.py:607-629``).  Row b's padding tokens sit at positions len_b.. past its prompt: their K/V go
+        to offsets past len_b of its last page (overwritten by its next decode appends, never read below its
+        length) or, past that page, to one padding page that only padding rows read; the causal mask keeps every
+        prompt token's attention inside its own prompt.  Each session ends holding exactly its prompt, and the
+        logits of padding positions are returned as zeros."""
+        lens = [len(t) for t in batches]
+        B, L, P = len(caches), max(lens), self.kv_allocator.page_size
+        ids = np.zeros((B, L), dtype=np.int64)
+        for b, toks in enumerate(batches):
+            ids[b, : len(toks)] = toks
+        real = np.concatenate([np.asarray(t, dtype=np.int64) for t in batches])
+        if int(real.min()) < 0 or int(real.max()) >= self.config.vocab_size:
+            bad = int(real.min()) if int(real.min()) < 0 else int(real.max())
+            raise IndexError(f"token id {bad} is out of range for vocabulary size {self.config.vocab_size}")
+        width = -(-L // P)
+        self.kv_allocator.reserve(sum(-(-n // P) for n in lens) + 1)
+        pad_slot = self.kv_allocator.allocate("prefill-padding")
+        try:
+            for c, n in zip(caches, lens):
+                c.ensure_capacity(c.tokens + n)
+            max_pages = self._bucket(width)
+            rows = np.zeros((B, max_pages), dtype=np.int32)
+            for b, c in enumerate(caches):
+                own = c.slot_array()
+                rows[b, : len(own)] = own
+                rows[b, len(own): width] = pad_slot
+            positions = np.fromiter((c.tokens for c in caches), dtype=np.int32, count=B)
+            self._enforce_memory_limit()
+            try:
+                plan = self.plan("prefill", B, L, max_pages)
+                plan.set_inputs(ids, rows, positions)
+                plan.launch()
+            except torch.cuda.OutOfMemoryError as exc:
+                self._recover_from_oom()
+                raise RuntimeError("CacheIR HIP runtime recovered from an out-of-memory condition; "
+                                   "retry with fewer or shorter prompts") from exc
+        finally:
+            # stream ordered: a later user of the slot writes it only after this step's padding writes
+            self.kv_allocator.release([pad_slot])
+        for c, n in zip(caches, lens):
+            c.tokens += n
+        out = plan.logits.view(B, L, -1).clone()
+        for b, n in enumerate(lens):
+            if n < L:
+                out[b, n:] = 0
+        self._count("rocm.prefill_padded_batch")
         return out
 
     def prefill_tokens(self, token_ids, *, use_prefix_cache: bool = False, remember_prefix: bool = False):
@@ -828,6 +890,18 @@ class HipRuntime:
         slots = list(self.kv_cache.slots[:pages])
         self.kv_allocator.share(slots)
         self.prefix_cache.put(ids, PrefixPages(self.kv_allocator, slots, len(ids)))
+
+    def load_longest_prefix(self, token_ids) -> tuple[int, ...]:
+        """``cuda.py:677-681``: make the longest cached prefix of ``token_ids`` this session's KV (its pages aliased,
+        not copied, replacing what the session held) and return it; ``()`` when no cached prefix matches."""
+        prefix, pages = self.prefix_cache.longest_prefix([int(t) for t in token_ids])
+        if pages is None:
+            return ()
+        if pages.allocator is not self.kv_allocator:
+            raise ValueError("the cached prefix lives in another KV allocator (share one through fork())")
+        self._clear_rows()
+        self.kv_cache.alias_prefix(pages.slots, len(prefix))
+        return tuple(prefix)
 
     def decode_greedy(self, sessions: list["HipRuntime"], token_ids) -> list[int]:
         """One decode step for ``sessions`` (one token each) returning the greedy next ids instead of logits
@@ -873,6 +947,7 @@ class HipRuntime:
             f"{mode}:b{batch}:q{q_len}:p{pages}": {"captured": sorted(plan.graphs), "replays": plan.replays,
                                                   "launches": len(plan.launches)}
             for (mode, batch, q_len, pages), plan in self._plans.items() if plan.graphs}
+        stats["step_plans"] = {"cached": len(self._plans), "max": self.max_plans, "evictions": self.plan_evictions}
         stats["oom_recoveries"] = self.oom_recoveries
         stats["memory_limit_mb"] = self.memory_limit_mb
         stats["weight_bytes"] = self.weights.nbytes()

@@ -100,12 +100,14 @@ class GGUFFile:
             nbytes = count * 2
         else:
             raise NotImplementedError(f"GGUF tensor {name!r} has type {t}; the ROCm backend reads F32, F16, Q4_0, Q8_0")
+        # read into a writable array of our own (torch.from_numpy warns on read-only buffers)
+        data = np.empty(nbytes, dtype=np.uint8)
         with self.path.open("rb") as f:
             f.seek(self.data_offset + info["offset"])
-            data = f.read(nbytes)
-        if len(data) != nbytes:
+            got = f.readinto(memoryview(data))
+        if got != nbytes:
             raise ValueError(f"GGUF tensor {name!r} ended early")
-        return np.frombuffer(data, dtype=np.uint8)
+        return data
 
     def dense(self, name: str) -> np.ndarray:
         t = self.ggml_type(name)

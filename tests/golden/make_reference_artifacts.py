@@ -12,6 +12,12 @@
   fixed 7 x 37 matrix (odd width: the last byte of each 4-bit row holds one nibble) whose rows include exact
   halves, so np.round's half-to-even rule decides zero points and codes; packed bytes, scales, zero points and
   ``dequantize_packed_weight``'s output.
+* ``reference_artifact_tiny_gguf_q4_0.json`` / ``..._q8_0.json``: the artifact ``compile_model`` writes for the
+  tiny model stored as a GGUF file (``tiny_gguf.py``: Q4_0 or Q8_0 linear weights, F16 embedding, F32 norms,
+  ``llama.*`` metadata), i.e. the config built from GGUF metadata (cacheir/compiler.py:40-63) and weight specs
+  keyed by GGUF tensor names (compiler.py:66-107).  Each also records the GGUF file's SHA-256 and the reference
+  NumPy backend's 32 greedy ids and top-2 margins on it (the blocks decoded by GGUFReader.read_tensor,
+  cacheir/runtime/cpu.py:60-68, then the greedy loop of cpu.py:167-184).
 
 Only this script reads /root/reference; it runs with the working directory outside this repository (the
 reference's native-extension search path then finds nothing and its NumPy branches run).
@@ -26,8 +32,13 @@ from pathlib import Path
 
 import numpy as np
 
-REF = Path(os.environ.get("CACHEIR_REFERENCE", "/root/reference"))
+sys.dont_write_bytecode = True  # importing the reference must leave no __pycache__ in its tree
 HERE = Path(__file__).resolve().parent
+sys.path.insert(0, str(HERE.parents[1]))  # the repo root: oracle/ and tests/golden/tiny_gguf.py
+sys.path.insert(0, str(HERE))
+import tiny_gguf  # noqa: E402
+
+REF = Path(os.environ.get("CACHEIR_REFERENCE", "/root/reference"))
 CFG = dict(seed=0, vocab_size=1024, hidden_size=256, intermediate_size=688, num_layers=2, num_attention_heads=4,
            num_key_value_heads=2)
 
@@ -43,6 +54,20 @@ def pack_matrix() -> np.ndarray:
     # row 2: constant row (scale clamps to 1e-8)
     w[2] = 0.5
     return w
+
+
+def greedy(rt, prompt: list[int], steps: int = 32) -> tuple[list[int], list[float]]:
+    """cpu.py:167-184 on the reference Runtime ``rt``: ids and each step's top-2 margin."""
+    logits = rt.run([prompt], mode="prefill")
+    ids, margins = [], []
+    for _ in range(steps):
+        last = np.asarray(logits[0, -1], dtype=np.float64)
+        top = np.sort(last)[-2:]
+        nxt = int(np.argmax(last)) % 1024
+        ids.append(nxt)
+        margins.append(float(top[1] - top[0]))
+        logits = rt.run([[nxt]], mode="decode")
+    return ids, margins
 
 
 def main() -> None:
@@ -62,17 +87,21 @@ def main() -> None:
             # the per-pass graph snapshots (~0.5 MB, read by no runtime) are cut to each mode's first two entries
             d["pass_traces"] = {m: list(t)[:2] for m, t in d["pass_traces"].items()}
             if quant:
-                rt = Runtime(art)
-                logits = rt.run([prompt], mode="prefill")
-                ids, margins = [], []
-                for _ in range(32):
-                    last = np.asarray(logits[0, -1], dtype=np.float64)
-                    top = np.sort(last)[-2:]
-                    nxt = int(np.argmax(last)) % 1024
-                    ids.append(nxt)
-                    margins.append(float(top[1] - top[0]))
-                    logits = rt.run([[nxt]], mode="decode")
+                ids, margins = greedy(Runtime(art), prompt)
                 d["fixture"] = {"prompt": prompt, "greedy_ids": ids, "top2_margins": margins}
+            (HERE / name).write_text(json.dumps(d, indent=1) + "\n", encoding="utf-8")
+            print(f"wrote {name}")
+
+        for fmt in ("q4_0", "q8_0"):
+            gguf = Path(tmp) / f"tiny_{fmt}.gguf"
+            sha = tiny_gguf.write_tiny_gguf(gguf, fmt)
+            art = compile_model(gguf, target="cpu", mode=["prefill", "decode"], max_seq=256)
+            ids, margins = greedy(Runtime(art), prompt)
+            d = art.to_dict()
+            d["model_path"] = ""
+            d["pass_traces"] = {m: list(t)[:2] for m, t in d["pass_traces"].items()}
+            d["fixture"] = {"prompt": prompt, "greedy_ids": ids, "top2_margins": margins, "gguf_sha256": sha}
+            name = f"reference_artifact_tiny_gguf_{fmt}.json"
             (HERE / name).write_text(json.dumps(d, indent=1) + "\n", encoding="utf-8")
             print(f"wrote {name}")
 

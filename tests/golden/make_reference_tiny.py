@@ -24,6 +24,8 @@ from pathlib import Path
 
 import numpy as np
 
+sys.dont_write_bytecode = True  # importing the reference must leave no __pycache__ in its tree
+
 REF = Path(os.environ.get("CACHEIR_REFERENCE", "/root/reference"))
 OUT = Path(__file__).resolve().parent / "reference_tiny.json"
 CFG = dict(seed=0, vocab_size=1024, hidden_size=256, intermediate_size=688, num_layers=2, num_attention_heads=4,

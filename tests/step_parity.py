@@ -1,0 +1,48 @@
+"""The step-level parity criterion shared by the config-4 and config-5 GPU tests (not a test module).
+
+A full decode step's logits cannot meet the per-kernel fp16 bound (2e-3 + 1e-2 |ref|) pointwise against the fp32
+oracle: storing GEMM inputs and q/k/v in fp16 perturbs them by ~3e-4, and the attention softmax of a random network
+amplifies that to ~2e-3 of the logits' rms.  So the step is held to two things:
+
+* relative: the HIP logits are no further from the fp32 oracle than the oracle's own fp16-storage variant is
+  (rms within 1.5x, max within 2x), closer still to the fp16-storage oracle (rms within 1x), and they pick the same
+  greedy id wherever the fp32 top-2 margin exceeds twice that noise;
+* absolute: against the fp16-storage oracle, which rounds where the kernels store fp16, at most ``out_cap`` of the
+  logits fall outside the per-kernel bound 2e-3 + 1e-2 |ref| -- a fixed number, so a wiring error of the size of
+  an fp16 rounding that the relative test would absorb still fails here.
+
+Every ratio is printed, so a run shows how much room each test had.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+
+def rms(a: np.ndarray) -> float:
+    return float(np.sqrt(np.mean(np.square(a))))
+
+
+def check_step(tag: str, got: np.ndarray, ref16: np.ndarray, ref32: np.ndarray, batch: int,
+               out_cap: float = 0.002) -> None:
+    got, ref16, ref32 = (np.asarray(a, np.float64) for a in (got, ref16, ref32))
+    assert np.isfinite(got).all()
+    noise_rms, noise_max = rms(ref16 - ref32), float(np.abs(ref16 - ref32).max())
+    d32, d16 = got - ref32, got - ref16
+    bound16 = 2e-3 + 1e-2 * np.abs(ref16)
+    out16 = float(np.mean(np.abs(d16) > bound16))
+    out32 = float(np.mean(np.abs(d32) > 2e-3 + 1e-2 * np.abs(ref32)))
+    r = {"rms32": rms(d32) / noise_rms, "max32": float(np.abs(d32).max()) / noise_max, "rms16": rms(d16) / noise_rms,
+         "worst16": float((np.abs(d16) / bound16).max())}
+    print(f"{tag}: logits rms {rms(ref32):.3f}; fp16-storage oracle vs fp32: rms {noise_rms:.3e} max {noise_max:.3e}; "
+          f"HIP vs fp32: rms {rms(d32):.3e} max {np.abs(d32).max():.3e}; HIP vs fp16-storage: rms {rms(d16):.3e} "
+          f"max {np.abs(d16).max():.3e}", flush=True)
+    print(f"{tag}: ratios rms32 {r['rms32']:.3f} (<= 1.5), max32 {r['max32']:.3f} (<= 2), rms16 {r['rms16']:.3f} "
+          f"(<= 1); outside the per-kernel bound: {out16:.2e} of the logits vs the fp16-storage oracle "
+          f"(<= {out_cap}), {out32:.2e} vs fp32 (reported); worst |d16| / bound {r['worst16']:.3f}", flush=True)
+    assert r["rms32"] <= 1.5 and r["max32"] <= 2.0
+    assert r["rms16"] <= 1.0
+    assert out16 <= out_cap, f"{out16:.3e} of the logits outside 2e-3 + 1e-2|ref| of the fp16-storage oracle"
+    top2 = np.sort(ref32, axis=1)[:, -2:]
+    clear = (top2[:, 1] - top2[:, 0]) > 2 * noise_max
+    assert clear.sum() >= batch // 2, f"only {clear.sum()} rows with a clear greedy margin"
+    assert np.array_equal(got.argmax(axis=1)[clear], ref32.argmax(axis=1)[clear])

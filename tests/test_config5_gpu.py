@@ -5,7 +5,8 @@ page table, per-request suffixes uniform in [64, 7168]) through HipRuntime on th
   weight Q8_0) cut to 1 layer so the oracle finishes in seconds; the full batch and contexts.  One
   ``run_decode_batch`` step (a replayed HIP graph) against ``OracleRuntime``'s ragged decode (each row over its
   own cache, RoPE at its own position) on the decoded blocks and the same K/V context, judged as the config-4
-  test judges its step: no further from the fp32 oracle than the fp16-storage oracle is, and the same greedy ids
+  test judges its step (``step_parity.check_step``): no further from the fp32 oracle than the fp16-storage
+  oracle is, at most 0.2% of the logits outside 2e-3 + 1e-2 |ref| of that oracle, and the same greedy ids
   wherever the fp32 top-2 margin is clear of that noise.
 * Full size: the 28-layer model, through properties the oracle cannot afford: finite logits, the fused greedy
   head's ids equal the argmax of the logits, the captured step equals the eager launches bitwise, and the
@@ -18,6 +19,7 @@ import pytest
 import torch
 
 from oracle import quant as oq
+from step_parity import check_step
 from oracle.runtime import OracleRuntime
 
 pytestmark = pytest.mark.gpu
@@ -150,21 +152,7 @@ def test_config5_one_layer_matches_oracle(device):
             orc.values[layer] = [a.copy() for a in ctx_v[layer]]
         refs[fp16_storage] = orc.run(ids[:, None], mode="decode")[:, 0].astype(np.float64)
         print(f"config5-1L: oracle (fp16 storage {fp16_storage}) done {time.time() - t0:.1f}s", flush=True)
-    assert np.isfinite(got).all()
-    # the criterion of the config-4 test (the fp16-storage oracle's distance from the fp32 one is the step's noise)
-    ref16, ref32 = refs[True], refs[False]
-    rms = lambda a: float(np.sqrt(np.mean(a ** 2)))
-    noise_rms, noise_max = rms(ref16 - ref32), float(np.abs(ref16 - ref32).max())
-    d32, d16 = got - ref32, got - ref16
-    print(f"config5-1L: logits rms {rms(ref32):.3f}; fp16-storage oracle vs fp32: rms {noise_rms:.3e} max "
-          f"{noise_max:.3e}; HIP vs fp32: rms {rms(d32):.3e} max {np.abs(d32).max():.3e}; HIP vs fp16-storage: "
-          f"rms {rms(d16):.3e} max {np.abs(d16).max():.3e}", flush=True)
-    assert rms(d32) <= 1.5 * noise_rms and np.abs(d32).max() <= 2.0 * noise_max
-    assert rms(d16) <= noise_rms
-    top2 = np.sort(ref32, axis=1)[:, -2:]
-    clear = (top2[:, 1] - top2[:, 0]) > 2 * noise_max
-    assert clear.sum() >= B // 2, f"only {clear.sum()} rows with a clear greedy margin"
-    assert np.array_equal(got.argmax(axis=1)[clear], ref32.argmax(axis=1)[clear])
+    check_step("config5-1L", got, refs[True], refs[False], B)
 
 
 def test_config5_full_size_properties(device):

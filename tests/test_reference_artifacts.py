@@ -10,8 +10,15 @@
   and their decode/prefill graphs have exactly the node list, op names, value names and weight keys that
   ``compile_config`` builds -- the graph HipRuntime executes.  (Running them on the GPU is
   tests/test_reference_artifacts_gpu.py.)
+* ``reference_artifact_tiny_gguf_{q4_0,q8_0}.json``: what ``compile_model`` writes for a GGUF file (config from
+  GGUF metadata, cacheir/compiler.py:40-63; weight specs keyed by GGUF tensor names, compiler.py:66-107), with
+  the reference NumPy backend's greedy ids on it.  The file ``tests/golden/tiny_gguf.py`` builds must be the
+  file the reference ran (SHA-256); this backend's GGUF reader returns every tensor the specs name, in the
+  shape they state, with the blocks' bytes as stored; and the oracle run on the decoded blocks reproduces all
+  32 of the reference's ids.
 """
 import json
+import sys
 from pathlib import Path
 
 import numpy as np
@@ -19,10 +26,13 @@ import pytest
 
 from cacheir_amd import CompileArtifact, retarget
 from cacheir_amd.compiler import compile_config
-from cacheir_amd.weights import pack_rows, unpack_rows
+from cacheir_amd.weights import GGUFFile, pack_rows, unpack_rows
 from oracle import quant as oq
+from oracle.runtime import OracleRuntime
 
 GOLDEN = Path(__file__).resolve().parent / "golden"
+sys.path.insert(0, str(GOLDEN))
+import tiny_gguf  # noqa: E402
 PACK = json.loads((GOLDEN / "reference_pack.json").read_text())
 
 
@@ -75,3 +85,34 @@ def test_reference_artifact_retargets_to_the_graph_the_runtime_runs(name, quant)
                 if key in m.attrs:
                     assert n.attrs.get(key) == m.attrs[key], (n.name, key)
         assert g.attrs["execution_hints"]["page_size"] == 16
+
+
+@pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
+def test_reference_gguf_artifact_loads_and_the_oracle_reproduces_its_ids(fmt, tmp_path):
+    d = json.loads((GOLDEN / f"reference_artifact_tiny_gguf_{fmt}.json").read_text())
+    fx = d.pop("fixture")
+    path = tmp_path / f"tiny_{fmt}.gguf"
+    assert tiny_gguf.write_tiny_gguf(path, fmt) == fx["gguf_sha256"]
+    art = CompileArtifact.from_dict(d)
+    assert art.quant is None and art.config.quantization == "gguf" and art.config.dtype == "float16"
+    assert art.config.hidden_size == tiny_gguf.CFG["hidden_size"] and art.config.num_layers == 2
+    retarget(art)
+    assert art.target == "rocm"
+    f = GGUFFile(path)
+    code = oq.GGML_TYPE_Q4_0 if fmt == "q4_0" else oq.GGML_TYPE_Q8_0
+    for mode in ("prefill", "decode"):
+        g = art.graph(mode)
+        assert all(n.attrs["kernel"].startswith("rocm.") for n in g.nodes)
+        for name, spec in g.weights.items():
+            assert spec.key in f.tensors, (name, spec.key)
+            assert f.shape(spec.key) == tuple(spec.tensor_type.shape), spec.key
+            if len(spec.tensor_type.shape) == 2 and spec.key != "token_embd.weight":
+                assert f.ggml_type(spec.key) == code  # the blocks load packed, as stored
+    w = tiny_gguf.decoded_weights(fmt)
+    orc = OracleRuntime({m: art.graph(m).to_dict() for m in ("prefill", "decode")}, w, art.config.vocab_size)
+    logits = orc.run([fx["prompt"]], mode="prefill")
+    ids = []
+    for want in fx["greedy_ids"]:  # teacher forced, so one early flip cannot hide the rest
+        ids.append(int(np.argmax(logits[0, -1])))
+        logits = orc.run([[want]], mode="decode")
+    assert ids == fx["greedy_ids"]

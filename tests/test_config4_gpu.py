@@ -4,7 +4,7 @@
   linear weight Q4_0) cut to 2 layers so the oracle finishes in seconds, batch 32, every sequence at 2048 tokens
   of context over pages scattered through the pool.  One ``run_decode_batch`` step (a replayed HIP graph) against
   ``OracleRuntime`` on the decoded blocks with the same K/V context, held to ``step_parity.check_step``: no
-  further from the fp32 oracle than the oracle's fp16-storage variant is, at most 0.2% of the logits outside
+  further from the fp32 oracle than the oracle's fp16-storage variant is, at most 2% of the logits outside
   2e-3 + 1e-2 |ref| of that variant, and greedy ids equal wherever the oracle's top-2 margin exceeds twice the
   fp16 noise.
 * Full size: the 32-layer model, through properties the oracle cannot afford: finite logits, the fused greedy

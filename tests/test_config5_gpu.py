@@ -6,7 +6,7 @@ page table, per-request suffixes uniform in [64, 7168]) through HipRuntime on th
   ``run_decode_batch`` step (a replayed HIP graph) against ``OracleRuntime``'s ragged decode (each row over its
   own cache, RoPE at its own position) on the decoded blocks and the same K/V context, judged as the config-4
   test judges its step (``step_parity.check_step``): no further from the fp32 oracle than the fp16-storage
-  oracle is, at most 0.2% of the logits outside 2e-3 + 1e-2 |ref| of that oracle, and the same greedy ids
+  oracle is, at most 2% of the logits outside 2e-3 + 1e-2 |ref| of that oracle, and the same greedy ids
   wherever the fp32 top-2 margin is clear of that noise.
 * Full size: the 28-layer model, through properties the oracle cannot afford: finite logits, the fused greedy
   head's ids equal the argmax of the logits, the captured step equals the eager launches bitwise, and the

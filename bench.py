@@ -291,6 +291,38 @@ def ragged_attention_case(config: int, dev, iters: int) -> dict:
     return res
 
 
+def read_ceiling(dev, sizes: dict[str, int], iters: int = 24) -> dict:
+    """Best rate of a plain read of each byte count (``cir_stream_read``): grid-stride and chunked layouts over
+    224-2048 workgroups of 256 or 512 threads, each launch reading a different buffer of a set larger than the
+    256 MB MALL.  The hot kernels' rates are read against these as well as against the 8 TB/s peak."""
+    import torch
+    from cacheir_amd import kernels
+
+    out = torch.zeros(1, dtype=torch.int32, device=dev)
+    res = {}
+    for name, nbytes in sizes.items():
+        nbytes = nbytes // 16 * 16
+        copies = max(4, -(-1_500_000_000 // nbytes))
+        bufs = [torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(c + 1) for c in range(copies)]
+        best = None
+        for layout in (0, 1):
+            for wgs in (224, 256, 512, 1024, 2048):
+                for threads in (256, 512):
+                    us = graph_us_per_launch(
+                        lambda i: kernels.stream_read(bufs[i % copies], wgs, threads, layout, out), iters)
+                    if best is None or us < best[0]:
+                        best = (us, layout, wgs, threads)
+        us, layout, wgs, threads = best
+        gbs = nbytes / (us * 1e-6) / 1e9
+        res[name] = {"bytes": nbytes, "us": round(us, 3), "gbs": round(gbs, 1), "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4),
+                     "shape": f"{'grid-stride' if layout == 0 else 'chunked'} {wgs} x {threads}"}
+        log(f"read ceiling {name}: {nbytes / 1e6:.1f} MB in {us:.2f} us = {gbs:.0f} GB/s "
+            f"({gbs / HBM_PEAK_GBS:.1%} of peak; {res[name]['shape']})")
+        del bufs
+        torch.cuda.empty_cache()
+    return res
+
+
 def prefill_case(base, cfg, tokens: int, dev) -> dict:
     """Prefill measured (the step before decode): one prompt of ``tokens`` ids through ``HipRuntime.run`` on the
     base session (causal paged attention writing the pool, projections on the large-m MFMA GEMM, logits for every
@@ -607,6 +639,10 @@ def main() -> int:
         f"({c5['frac_of_floor']:.1%} of its {c5['hbm_floor_ms']:.2f} ms HBM floor)")
 
     traffic = measured_traffic(TRAFFIC_FILE)
+    ceiling = read_ceiling(dev, {"attention": attn_bytes, "gate_up": gemm_bytes,
+                                 "config3": gemv[0]["bytes_per_launch"] if gemv else 33075200})
+    for row in gemv:  # config-3 projections against the read of their own size (33.0-35.1 MB, one ceiling)
+        row["frac_of_read_ceiling"] = round(row["achieved"] / ceiling["config3"]["gbs"], 4)
 
     # ---- CPU baseline: C/OpenMP restatement, one layer + lm_head, scaled to the step ----
     cpu = None
@@ -636,7 +672,11 @@ def main() -> int:
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic["bytes"] if traffic else None,
                      "traffic_detail": traffic,
-                     "bytes_per_launch": attn_bytes, "us_per_launch": round(attn_us, 3)},
+                     "bytes_per_launch": attn_bytes, "us_per_launch": round(attn_us, 3),
+                     "frac_of_read_ceiling": round(achieved / ceiling["attention"]["gbs"], 4)},
+        "read_ceiling": {"note": "best plain read of each byte count on this GPU (cir_stream_read, buffers rotated "
+                                 "past the MALL): what a kernel moving those bytes could reach at most",
+                         **ceiling},
         "roofline_attention_ragged": {"bound": "hbm", "peak": HBM_PEAK_GBS, "unit": "GB/s",
                                       "note": "BASELINE configs 2 and 5; achieved on unique K/V bytes (config 5's "
                                               "shared prefix counted once), logical bytes beside it",
@@ -645,6 +685,7 @@ def main() -> int:
                           "achieved": round(gemm_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                           "frac": round(gemm_gbs / HBM_PEAK_GBS, 4), "bytes_per_launch": gemm_bytes,
                           "us_per_launch": round(gemm_us, 3),
+                          "frac_of_read_ceiling": round(gemm_gbs / ceiling["gate_up"]["gbs"], 4),
                           "counters": measured_counters(COUNTERS_FILE, "xs_swiglu")},
         "roofline_gemv": {"bound": "hbm", "kernel": "Q4_0 projections, BASELINE config 3 (n x k, y = x W^T): dequant "
                                                     "GEMV at m <= 8, MFMA GEMM at m = 32",

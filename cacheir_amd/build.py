@@ -18,7 +18,7 @@ SRC = PKG / "csrc"
 OBJ = PKG / "_build"
 LIB_DIR = PKG / "_lib"
 LIB = LIB_DIR / "libcacheir_hip.so"
-SOURCES = ["attention.hip", "qgemm.hip", "rowops.hip"]
+SOURCES = ["attention.hip", "qgemm.hip", "rowops.hip", "probe.hip"]
 ARCH = os.environ.get("CACHEIR_HIP_ARCH", "gfx950")
 
 

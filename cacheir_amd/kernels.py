@@ -460,3 +460,11 @@ def argmax(logits: torch.Tensor, out=None) -> torch.Tensor:
         out = torch.empty(rows, dtype=torch.int64, device=logits.device)
     hip.call("cir_argmax", logits.data_ptr(), vocab, out.data_ptr(), rows, vocab, hip.stream_handle())
     return out
+
+
+def stream_read(buf: torch.Tensor, workgroups: int, threads: int, layout: int, out: torch.Tensor) -> None:
+    """Read every byte of ``buf`` (``cir_stream_read``; read-bandwidth calibration, not on the decode path)."""
+    _cuda(buf, "buf")
+    _cuda(out, "out")
+    hip.call("cir_stream_read", buf.data_ptr(), buf.numel() * buf.element_size(), int(workgroups), int(threads),
+             int(layout), out.data_ptr(), hip.stream_handle())

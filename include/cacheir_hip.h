@@ -288,6 +288,15 @@ size_t cir_qgemm_argmax_workspace_bytes(int m, int n);
 int cir_qgemm_argmax(const void* x, int ldx, const void* w_tiled, int fmt, int64_t* ids, void* workspace,
                      size_t ws_bytes, int m, int n, int k, void* stream);
 
+/* ------------------------------------------------------------- calibration ---
+ * Reads `bytes` (a multiple of 16) from buf with `workgroups` x `threads` threads,
+ * grid-stride (layout 0) or one contiguous chunk per workgroup (layout 1), and writes
+ * nothing but an unreachable sentinel to out (one uint32).  No counterpart in the
+ * reference: it measures what a plain read of a hot kernel's byte count reaches on
+ * this GPU, the ceiling the roofline fractions are read against. */
+int cir_stream_read(const void* buf, size_t bytes, int workgroups, int threads, int layout, void* out,
+                    void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -849,3 +849,18 @@ def test_qgemm_argmax_matches_gemm_then_argmax(device, fmt, m, k):
         assert got[4] == 0
     # the fused kernel's ids also equal cir_argmax over the same logits
     assert np.array_equal(kernels.argmax(logits).cpu().numpy(), want)
+
+
+def test_stream_read_calibration_runs(device):
+    """cir_stream_read (the bench's read ceiling) reads a buffer in both layouts and leaves its output alone."""
+    from cacheir_amd import kernels
+
+    buf = torch.arange(1 << 20, dtype=torch.int32, device=device)
+    out = torch.zeros(1, dtype=torch.int32, device=device)
+    for layout in (0, 1):
+        for wgs, threads in ((224, 256), (1024, 512), (7, 64)):
+            kernels.stream_read(buf, wgs, threads, layout, out)
+    torch.cuda.synchronize()
+    assert int(out.item()) == 0
+    with pytest.raises(Exception):
+        kernels.stream_read(buf, 0, 256, 0, out)

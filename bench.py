@@ -291,6 +291,39 @@ def ragged_attention_case(config: int, dev, iters: int) -> dict:
     return res
 
 
+def read_ceiling_mixed(dev, nbytes: int, side_bytes: int, side_ratio: int, iters: int = 24) -> dict:
+    """The same best-shape read of ``nbytes`` with ``side_ratio`` reads of an L2-resident ``side_bytes`` buffer per 8
+    chunks streamed (all issued before any is consumed): the loads of the m = 32 gate|up GEMM, whose 224
+    workgroups each re-read the 256 KB of activations beside their share of the weights (side_ratio 7: 0.875 bytes
+    of activations per weight byte)."""
+    import torch
+    from cacheir_amd import kernels
+
+    out = torch.zeros(1, dtype=torch.int32, device=dev)
+    nbytes = nbytes // 16 * 16
+    copies = max(4, -(-1_500_000_000 // nbytes))
+    bufs = [torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(c + 1) for c in range(copies)]
+    side = torch.ones(side_bytes, dtype=torch.uint8, device=dev)
+    best = None
+    for layout in (0, 1):
+        for wgs in (224, 256, 512):
+            for threads in (256, 512):
+                us = graph_us_per_launch(lambda i: kernels.stream_read(bufs[i % copies], wgs, threads, layout, out,
+                                                                       side=side, side_ratio=side_ratio), iters)
+                if best is None or us < best[0]:
+                    best = (us, layout, wgs, threads)
+    us, layout, wgs, threads = best
+    side_total = nbytes * side_ratio // 8
+    res = {"bytes": nbytes, "side_bytes_read": side_total, "us": round(us, 3),
+           "gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
+           "shape": f"{'grid-stride' if layout == 0 else 'chunked'} {wgs} x {threads}"}
+    log(f"read ceiling with L2 re-reads: {nbytes / 1e6:.1f} MB + {side_total / 1e6:.1f} MB from a "
+        f"{side_bytes // 1024} KB buffer in {us:.2f} us = {res['gbs']:.0f} GB/s of the stream ({res['shape']})")
+    del bufs
+    torch.cuda.empty_cache()
+    return res
+
+
 def read_ceiling(dev, sizes: dict[str, int], iters: int = 24) -> dict:
     """Best rate of a plain read of each byte count (``cir_stream_read``): grid-stride and chunked layouts over
     224-2048 workgroups of 256 or 512 threads, each launch reading a different buffer of a set larger than the
@@ -641,6 +674,8 @@ def main() -> int:
     traffic = measured_traffic(TRAFFIC_FILE)
     ceiling = read_ceiling(dev, {"attention": attn_bytes, "gate_up": gemm_bytes,
                                  "config3": gemv[0]["bytes_per_launch"] if gemv else 33075200})
+    # the activations the gate|up GEMM re-reads: B rows x hidden fp16 = 256 KB at batch 32
+    ceiling["gate_up_with_activations"] = read_ceiling_mixed(dev, gemm_bytes, B * cfg.hidden_size * 2, 7)
     for row in gemv:  # config-3 projections against the read of their own size (33.0-35.1 MB, one ceiling)
         row["frac_of_read_ceiling"] = round(row["achieved"] / ceiling["config3"]["gbs"], 4)
 
@@ -686,6 +721,8 @@ def main() -> int:
                           "frac": round(gemm_gbs / HBM_PEAK_GBS, 4), "bytes_per_launch": gemm_bytes,
                           "us_per_launch": round(gemm_us, 3),
                           "frac_of_read_ceiling": round(gemm_gbs / ceiling["gate_up"]["gbs"], 4),
+                          "frac_of_read_ceiling_with_activations":
+                              round(gemm_gbs / ceiling["gate_up_with_activations"]["gbs"], 4),
                           "counters": measured_counters(COUNTERS_FILE, "xs_swiglu")},
         "roofline_gemv": {"bound": "hbm", "kernel": "Q4_0 projections, BASELINE config 3 (n x k, y = x W^T): dequant "
                                                     "GEMV at m <= 8, MFMA GEMM at m = 32",

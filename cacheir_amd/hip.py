@@ -62,7 +62,7 @@ _SIGNATURES = {
     "cir_epilogue_residual_rmsnorm": (_c_int, [_vp, _c_int, _vp, _vp, _vp, _c_int, _c_float, _vp, _c_int, _c_int,
                                                _c_int, _vp]),
     "cir_epilogue_swiglu": (_c_int, [_vp, _c_int, _vp, _c_int, _c_int, _c_int, _vp]),
-    "cir_stream_read": (_c_int, [_vp, _c_size, _c_int, _c_int, _c_int, _vp, _vp]),
+    "cir_stream_read": (_c_int, [_vp, _c_size, _c_int, _c_int, _c_int, _vp, _c_size, _c_int, _vp, _vp]),
     "cir_epilogue_qkv_rope_append": (_c_int, [_vp, _c_int, _vp, _vp, _vp, _c_int, _vp, _c_int, _vp, _vp, _c_int, _c_int,
                                               _c_int, _c_int, _c_int, _c_int, _c_int, _vp]),
     "cir_embedding": (_c_int, [_vp, _vp, _c_int, _vp, _c_int, _c_int, _c_int, _c_int, _vp]),

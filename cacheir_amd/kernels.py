@@ -462,9 +462,15 @@ def argmax(logits: torch.Tensor, out=None) -> torch.Tensor:
     return out
 
 
-def stream_read(buf: torch.Tensor, workgroups: int, threads: int, layout: int, out: torch.Tensor) -> None:
-    """Read every byte of ``buf`` (``cir_stream_read``; read-bandwidth calibration, not on the decode path)."""
+def stream_read(buf: torch.Tensor, workgroups: int, threads: int, layout: int, out: torch.Tensor,
+                side: torch.Tensor | None = None, side_ratio: int = 0) -> None:
+    """Read every byte of ``buf`` (``cir_stream_read``; read-bandwidth calibration, not on the decode path), with
+    ``side_ratio`` 16-byte reads of the L2-resident ``side`` per 8 of ``buf``."""
     _cuda(buf, "buf")
     _cuda(out, "out")
+    sp, sb = 0, 0
+    if side is not None:
+        _cuda(side, "side")
+        sp, sb = side.data_ptr(), side.numel() * side.element_size()
     hip.call("cir_stream_read", buf.data_ptr(), buf.numel() * buf.element_size(), int(workgroups), int(threads),
-             int(layout), out.data_ptr(), hip.stream_handle())
+             int(layout), sp, sb, int(side_ratio), out.data_ptr(), hip.stream_handle())

@@ -291,11 +291,14 @@ int cir_qgemm_argmax(const void* x, int ldx, const void* w_tiled, int fmt, int64
 /* ------------------------------------------------------------- calibration ---
  * Reads `bytes` (a multiple of 16) from buf with `workgroups` x `threads` threads,
  * grid-stride (layout 0) or one contiguous chunk per workgroup (layout 1), and writes
- * nothing but an unreachable sentinel to out (one uint32).  No counterpart in the
- * reference: it measures what a plain read of a hot kernel's byte count reaches on
- * this GPU, the ceiling the roofline fractions are read against. */
-int cir_stream_read(const void* buf, size_t bytes, int workgroups, int threads, int layout, void* out,
-                    void* stream);
+ * nothing but an unreachable sentinel to out (one uint32).  With side_ratio 1..8 each
+ * thread also reads side_ratio 16-byte chunks of `side` (side_bytes, a power of two of
+ * 16-byte chunks, small enough to stay in L2) per 8 chunks of buf, issued together:
+ * the load pattern of a GEMM that streams weights and re-reads activations.  No
+ * counterpart in the reference: it measures what a plain read of a hot kernel's bytes
+ * reaches on this GPU, the ceiling the roofline fractions are read against. */
+int cir_stream_read(const void* buf, size_t bytes, int workgroups, int threads, int layout, const void* side,
+                    size_t side_bytes, int side_ratio, void* out, void* stream);
 
 #ifdef __cplusplus
 }

@@ -860,7 +860,10 @@ def test_stream_read_calibration_runs(device):
     for layout in (0, 1):
         for wgs, threads in ((224, 256), (1024, 512), (7, 64)):
             kernels.stream_read(buf, wgs, threads, layout, out)
+            kernels.stream_read(buf, wgs, threads, layout, out, side=buf[: 1 << 16], side_ratio=3)
     torch.cuda.synchronize()
     assert int(out.item()) == 0
     with pytest.raises(Exception):
         kernels.stream_read(buf, 0, 256, 0, out)
+    with pytest.raises(Exception):  # the side buffer must hold a power of two of 16-byte chunks
+        kernels.stream_read(buf, 224, 256, 0, out, side=buf[:1000], side_ratio=2)

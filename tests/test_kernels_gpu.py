@@ -334,6 +334,68 @@ def test_qgemm_large_m_ragged_splits(device, fmt, m, n, k, splits):
     close16(part.sum(0), ops.matmul(x.astype(np.float32), wf.astype(np.float32)))
 
 
+@pytest.mark.parametrize("seed", range(12))
+def test_qgemm_planner_random_shapes(device, seed):
+    """Seeded random shapes through the planner's own choices (``choose_splits``, then whichever kernel
+    ``gemm_plan`` names: GEMV, the m <= 32 kernel with one or two row tiles, the large-m kernel at 64 or 128 rows
+    with splits that need not divide k/128): m in 1..200, ragged n up to ~5100, k up to 64 quads, both block
+    formats. The
+    partials' sum against the exact-product bound of fp64 and the fp16 bound of the oracle; the fused SwiGLU
+    (interleaved gate/up tiles) and the fused greedy head against the same products."""
+    from cacheir_amd import hip, kernels
+
+    rng = np.random.default_rng(900 + seed)
+    fmt = ("q4_0", "q8_0")[seed % 2]
+    code = kernels.FMT_NAMES[fmt]
+    enc, dec = (quant.random_q4_0, quant.decode_q4_0) if fmt == "q4_0" else (quant.random_q8_0, quant.decode_q8_0)
+    m = int(rng.choice([1, 2, 5, 8, 9, 16, 17, 31, 32, 33, 48, 64, 65, 100, 128, 129, 200]))
+    n = int(rng.integers(1, 321)) * 16 + int(rng.integers(0, 16))
+    k = 128 * int(rng.integers(1, 65))
+    inter = 16 * max(1, n // 32)
+    splits = kernels.choose_splits(m, n, k)
+    plan = kernels.gemm_plan(hip.GEMM_PARTIALS, code, m, n, k, splits)
+    plans = (plan, kernels.gemm_plan(hip.GEMM_SWIGLU, code, m, 2 * inter, k, 1),
+             kernels.gemm_plan(hip.GEMM_ARGMAX, code, m, n, k, 1))
+    print(f"seed {seed}: {fmt} m={m} n={n} k={k} splits={splits} -> {' | '.join(plans)}", flush=True)
+    assert "invalid" not in plans
+    blocks = enc(rng, n, k)[0]
+    wf = dec(blocks, k).astype(np.float64)
+    w = kernels.QWeight.from_blocks(to_dev(blocks.reshape(-1), device), code, n, k)
+    x = rng.standard_normal((m, k)).astype(np.float16)
+    xd = to_dev(x, device)
+    x64 = x.astype(np.float64)
+    got = kernels.qgemm_partial(xd, w, splits=splits).double().sum(0).cpu().numpy()
+    ref64 = x64 @ wf.T
+    assert np.all(np.abs(got - ref64) <= 1e-5 * (np.abs(x64) @ np.abs(wf).T) + 1e-6)
+    close16(got, ops.matmul(x.astype(np.float32), wf.astype(np.float32)))
+
+    # SwiGLU over interleaved gate/up tiles (inter columns each, a multiple of 16)
+    g_blocks, u_blocks = enc(rng, inter, k)[0], enc(rng, inter, k)[0]
+    g_dev, u_dev = to_dev(g_blocks, device), to_dev(u_blocks, device)
+    w_il = kernels.QWeight.from_blocks(kernels.interleave_gate_up(g_dev, u_dev, inter).reshape(-1), code, 2 * inter, k)
+    act = kernels.qgemm_swiglu(xd, w_il, torch.float32).double().cpu().numpy()
+    gw, uw = dec(g_blocks, k).astype(np.float64), dec(u_blocks, k).astype(np.float64)
+    g, u = x64 @ gw.T, x64 @ uw.T
+    sig = 1.0 / (1.0 + np.exp(-g))
+    want = g * sig * u
+    # g and u carry the exact-product bound of their fp32 sums; |d silu/dg| <= 1.1 carries it through
+    bg = 1e-5 * (np.abs(x64) @ np.abs(gw).T) + 1e-6
+    bu = 1e-5 * (np.abs(x64) @ np.abs(uw).T) + 1e-6
+    bound = 1.1 * bg * np.abs(u) + np.abs(g * sig) * bu + 1e-5 * np.abs(want) + 1e-6
+    assert np.all(np.abs(act - want) <= bound), np.abs(act - want).max()
+
+    # fused greedy head: the chosen column's product is the row maximum up to fp32 summation (ties resolve to
+    # the smallest column, so only rows whose top two products are apart are compared by id)
+    ids = torch.empty(m, dtype=torch.int64, device=device)
+    kernels.qgemm_argmax(xd, w, out=ids, workspace=kernels.qgemm_argmax_workspace(m, n, device))
+    ids = ids.cpu().numpy()
+    top2 = np.sort(ref64, axis=1)[:, -2:]
+    slack = 1e-5 * (np.abs(x64) @ np.abs(wf).T).max(axis=1) + 1e-6
+    assert np.all(ref64[np.arange(m), ids] >= top2[:, 1] - 2 * slack)
+    clear = (top2[:, 1] - top2[:, 0]) > 2 * slack
+    assert np.array_equal(ids[clear], ref64.argmax(axis=1)[clear])
+
+
 def test_gemm_f32(device):
     from cacheir_amd import kernels
 

@@ -396,6 +396,42 @@ def test_qgemm_planner_random_shapes(device, seed):
     assert np.array_equal(ids[clear], ref64.argmax(axis=1)[clear])
 
 
+@pytest.mark.parametrize("seed", range(8))
+def test_qgemm_planner_random_shapes_row_formats(device, seed):
+    """The same seeded sweep over the reference's per-row asymmetric int4/int8 packing (quantization.py; codes
+    times activations on MFMA, scale and zero point applied after the k loop): partials through the planner's
+    k-split and the fused greedy head, against fp64 on the dequantized weights within the fp16 bound."""
+    from cacheir_amd import hip, kernels
+
+    rng = np.random.default_rng(1900 + seed)
+    bits = (4, 8)[seed % 2]
+    code = hip.CIR_I4_ROW if bits == 4 else hip.CIR_I8_ROW
+    m = int(rng.choice([1, 3, 8, 9, 16, 17, 32, 33, 64, 100, 128, 129, 200]))
+    n = int(rng.integers(1, 321)) * 16 + int(rng.integers(0, 16))
+    k = 128 * int(rng.integers(1, 65))
+    splits = kernels.choose_splits(m, n, k)
+    plans = (kernels.gemm_plan(hip.GEMM_PARTIALS, code, m, n, k, splits), kernels.gemm_plan(hip.GEMM_ARGMAX, code, m, n, k, 1))
+    print(f"seed {seed}: int{bits} rows m={m} n={n} k={k} splits={splits} -> {' | '.join(plans)}", flush=True)
+    assert "invalid" not in plans
+    pk = quant.asymmetric_pack(rng.standard_normal((n, k)).astype(np.float32) * 0.05, bits)
+    w = kernels.QWeight.from_rows(to_dev(pk["packed_values"], device), to_dev(pk["scales"], device),
+                                  to_dev(pk["zero_points"], device), bits, n, k)
+    wd = quant.asymmetric_dequant(pk).astype(np.float64)
+    x = rng.standard_normal((m, k)).astype(np.float16)
+    xd = to_dev(x, device)
+    ref64 = x.astype(np.float64) @ wd.T
+    got = kernels.qgemm_partial(xd, w, splits=splits).double().sum(0).cpu().numpy()
+    close16(got, ref64)
+    ids = torch.empty(m, dtype=torch.int64, device=device)
+    kernels.qgemm_argmax(xd, w, out=ids, workspace=kernels.qgemm_argmax_workspace(m, n, device))
+    ids = ids.cpu().numpy()
+    top2 = np.sort(ref64, axis=1)[:, -2:]
+    slack = ATOL16 + RTOL16 * np.abs(top2[:, 1])
+    assert np.all(ref64[np.arange(m), ids] >= top2[:, 1] - 2 * slack)
+    clear = (top2[:, 1] - top2[:, 0]) > 2 * slack
+    assert np.array_equal(ids[clear], ref64.argmax(axis=1)[clear])
+
+
 def test_gemm_f32(device):
     from cacheir_amd import kernels
 

@@ -92,8 +92,10 @@ constexpr int kTiles = 2;             // 16-token MFMA tiles per wavefront step
 constexpr int kBlock = 16 * kTiles;   // tokens per wavefront step
 constexpr int kWaves = 8;             // wavefronts per workgroup (fp16 path)
 constexpr int kChunk = 128;  // tokens per partial in the generic path
-constexpr int kPtCache = 512;  // page-table entries a workgroup keeps in LDS (2 KiB)
-static_assert(64 * kWaves <= kPtCache, "one page-table entry per thread");
+// Page-table entries a workgroup keeps in LDS (2 KiB at 8 wavefronts): one per thread, since every thread fills
+// one entry (a split whose pages exceed the thread count reads the table directly); the row sort of the
+// longest-first dispatch also ranks one row per thread in this array.
+constexpr int kPtCache = 64 * kWaves;
 constexpr int kMinSplitTokens = 256;
 constexpr float kLog2e = 1.4426950408889634f;
 

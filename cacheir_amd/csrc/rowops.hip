@@ -137,10 +137,11 @@ __global__ __launch_bounds__(kEmbThreads) void embedding_kernel(const int64_t* _
 // Residual epilogue + RMSNorm of the result, one workgroup per row, 4 columns per
 // thread per step: h = residual + sum of partials (fp32, to h_out) and
 // xn = (h * rsqrt(mean(h^2) + eps)) * w.  N % 4 == 0 and N <= 8192; TWO (N > 4096)
-// gives each thread a second column group.  Its registers are compiled in only when the
-// host asks for it: with 16 splits they hold 2 x 16 float4 partials, 128 VGPRs, and
-// spill (a 9-split norm of 128 rows of 3584 took 10.2 us with them compiled in); rows
-// past 4096 with more than 8 splits still take that spilling variant.
+// gives each thread a second column group.  Every load of a column group (its partials,
+// the residual, the norm weights) is issued before the group's first add, so a row costs
+// one memory round trip; with more than 8 splits the two groups of a TWO row are loaded
+// and summed one after the other (two round trips): both groups' 16 float4 partials at
+// once would take 128 VGPRs and spill.
 template <int SMAX, bool TWO, typename TW, typename TO>
 __global__ __launch_bounds__(kRowThreads) void residual_rmsnorm_kernel(
     const float* __restrict__ part, int splits, const float* __restrict__ resid, float* __restrict__ h_out,
@@ -148,52 +149,63 @@ __global__ __launch_bounds__(kRowThreads) void residual_rmsnorm_kernel(
   __shared__ float scratch[kRowThreads / 64];
   const int r = blockIdx.x;
   const size_t plane = (size_t)M * N;
-  // Every load of the thread (partials of both column groups, residual, norm weights) is
-  // issued before the first add, so the row costs one memory round trip.
   constexpr int G = TWO ? 2 : 1;
-  const bool second = TWO;
-  float4 pv[G][SMAX], q[G], wv[G];
+  constexpr bool kSeq = TWO && SMAX > 8;
+  float4 v[G], wv[G];
   size_t idx[G];
   bool ok[G];
 #pragma unroll
   for (int i = 0; i < G; ++i) {
     const int c = 4 * (threadIdx.x + i * kRowThreads);
     ok[i] = c < N;
-    const int cc = ok[i] ? c : 0;
-    idx[i] = (size_t)r * N + cc;
-    if (i == 0 || second) {
-#pragma unroll
-      for (int sp = 0; sp < SMAX; ++sp)
-        pv[i][sp] = *reinterpret_cast<const float4*>(part + (sp < splits ? sp : 0) * plane + idx[i]);
-      q[i] = *reinterpret_cast<const float4*>(resid + idx[i]);
-      wv[i] = load4(w + cc);
-    }
+    idx[i] = (size_t)r * N + (ok[i] ? c : 0);
   }
-  float4 v[G];
-  float ss = 0.f;
+  auto load = [&](int i, float4 (&pv)[SMAX], float4& q) __attribute__((always_inline)) {
 #pragma unroll
-  for (int i = 0; i < G; ++i) {
+    for (int sp = 0; sp < SMAX; ++sp)
+      pv[sp] = *reinterpret_cast<const float4*>(part + (sp < splits ? sp : 0) * plane + idx[i]);
+    q = *reinterpret_cast<const float4*>(resid + idx[i]);
+    wv[i] = load4(w + (idx[i] - (size_t)r * N));
+  };
+  float ss = 0.f;
+  // partials in split order, then the residual (as split_sum4 + add)
+  auto fold = [&](int i, const float4 (&pv)[SMAX], const float4& q) __attribute__((always_inline)) {
     float4 t = {0.f, 0.f, 0.f, 0.f};
-    if ((i == 0 || second) && ok[i]) {
-      float4 p = pv[i][0];  // partials in split order, then the residual (as split_sum4 + add)
+    if (ok[i]) {
+      float4 p = pv[0];
 #pragma unroll
       for (int sp = 1; sp < SMAX; ++sp)
         if (sp < splits) {
-          p.x += pv[i][sp].x;
-          p.y += pv[i][sp].y;
-          p.z += pv[i][sp].z;
-          p.w += pv[i][sp].w;
+          p.x += pv[sp].x;
+          p.y += pv[sp].y;
+          p.z += pv[sp].z;
+          p.w += pv[sp].w;
         }
-      t = make_float4(q[i].x + p.x, q[i].y + p.y, q[i].z + p.z, q[i].w + p.w);
+      t = make_float4(q.x + p.x, q.y + p.y, q.z + p.z, q.w + p.w);
       *reinterpret_cast<float4*>(h_out + idx[i]) = t;
     }
     v[i] = t;
     ss += t.x * t.x + t.y * t.y + t.z * t.z + t.w * t.w;
+  };
+  if constexpr (kSeq) {
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+      float4 pv[SMAX], q;
+      load(i, pv, q);
+      fold(i, pv, q);
+      __builtin_amdgcn_sched_barrier(0);  // the next group's loads stay behind these sums
+    }
+  } else {
+    float4 pv[G][SMAX], q[G];
+#pragma unroll
+    for (int i = 0; i < G; ++i) load(i, pv[i], q[i]);
+#pragma unroll
+    for (int i = 0; i < G; ++i) fold(i, pv[i], q[i]);
   }
   const float scale = 1.0f / sqrtf(block_sum_1024(ss, scratch) / (float)N + eps);
 #pragma unroll
   for (int i = 0; i < G; ++i) {
-    if ((i == 0 || second) && ok[i])
+    if (ok[i])
       store4(xn + idx[i], make_float4((v[i].x * scale) * wv[i].x, (v[i].y * scale) * wv[i].y,
                                       (v[i].z * scale) * wv[i].z, (v[i].w * scale) * wv[i].w));
   }

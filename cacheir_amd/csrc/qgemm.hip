@@ -1182,11 +1182,14 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void qgemv_kernel(const f16* __
     for (int u = 0; u < XC; ++u) {
       const bool past = r >= M;
       const int rr = past ? M - 1 : r, cc = past ? cols16 - 1 : col;
-      if constexpr (XM)  // quad q of k is head q (head_dim 128)
-        xv[u] = attn_merged_chunk(ap, rr, q0 + (cc >> 4), 8 * (cc & 15));
-      else
-        xv[u] = *reinterpret_cast<const u32x4*>(x + (size_t)rr * ldx + 128 * q0 + 8 * cc);
       xoff[u] = rr * rs + 16 * (cc ^ (rr & 7));
+      if constexpr (XM) {  // quad q of k is head q (head_dim 128)
+        // The merge has waited for its loads already: its chunk goes to LDS at once rather
+        // than staying live across the weight prologue (eight such chunks per thread spill).
+        *reinterpret_cast<u32x4*>(&xs[xoff[u]]) = attn_merged_chunk(ap, rr, q0 + (cc >> 4), 8 * (cc & 15));
+      } else {
+        xv[u] = *reinterpret_cast<const u32x4*>(x + (size_t)rr * ldx + 128 * q0 + 8 * cc);
+      }
       r += r_step;
       col += c_step;
       if (col >= cols16) col -= cols16, ++r;
@@ -1223,8 +1226,10 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void qgemv_kernel(const f16* __
   };
   each.template operator()<DW>([&]<int S>() { issue(S); });
 
+  if constexpr (!XM) {
 #pragma unroll
-  for (int u = 0; u < XC; ++u) *reinterpret_cast<u32x4*>(&xs[xoff[u]]) = xv[u];
+    for (int u = 0; u < XC; ++u) *reinterpret_cast<u32x4*>(&xs[xoff[u]]) = xv[u];
+  }
   __syncthreads();
 
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -1455,6 +1460,12 @@ bool gemv_head_fits(int fmt, int m, int k) { return !is_row_fmt(fmt) && gemv_fit
 #define CIR_XS_KG 1
 #endif
 
+// Weight-ring depth of the m <= 32 kernel: 8-bit codes (two 16-byte loads per lane and tile) at 32 rows take 3
+// stages where the launch has two k-groups or the greedy epilogue; at 4 stages those need more than 256 VGPRs
+// and spill.
+template <int FMT, int MT, int EPI, int KG, int DW>
+inline constexpr int xs_ring = (layout_fmt(FMT) == CIR_Q8_0 && MT >= 2 && (KG >= 2 || EPI == 2) && DW > 3) ? 3 : DW;
+
 // k-groups per workgroup: a divisor of the split's quad count.  Two where a split has
 // 32 quads or more and the launch has at most one workgroup per CU, at any m
 // (measured: the unsplit gate|up + SwiGLU at k = 4096, 224 workgroups, gains ~4% at
@@ -1476,7 +1487,7 @@ void launch_qgemm_swiglu(const f16* x, int ldx, const uint8_t* wq, const uint16_
   const int NTILES = (N + 15) / 16;
   dim3 grid((NTILES + 7) / 8, 1, (M + 16 * MT - 1) / (16 * MT));
   auto go = [&]<int KG>() {
-    qgemm_xs_kernel<FMT, 2, MT, CIR_XS_DW_SWIGLU, 1, TO, KG>
+    qgemm_xs_kernel<FMT, 2, MT, xs_ring<FMT, MT, 1, KG, CIR_XS_DW_SWIGLU>, 1, TO, KG>
         <<<grid, 256 * KG, 0, s>>>(x, ldx, wq, wd, nullptr, M, N, K, K / 128, act);
   };
   const int kg = xs_kgroups(M, K / 128, (long)grid.x * grid.y * grid.z);
@@ -1545,7 +1556,7 @@ void launch_qgemm_argmax(const f16* x, int ldx, const uint8_t* wq, const uint16_
   dim3 grid((NTILES + 4 * NT - 1) / (4 * NT), 1, (M + 16 * MT - 1) / (16 * MT));
   const int quads = K / 128;
   auto go = [&]<int KG>() {
-    qgemm_xs_kernel<FMT, NT, MT, (MT == 1 ? 4 : CIR_XS_DW), 2, float, KG>
+    qgemm_xs_kernel<FMT, NT, MT, xs_ring<FMT, MT, 2, KG, (MT == 1 ? 4 : CIR_XS_DW)>, 2, float, KG>
         <<<grid, 256 * KG, 0, s>>>(x, ldx, wq, wd, cand_v, M, N, K, quads, reinterpret_cast<float*>(cand_i));
   };
   const int kg = xs_kgroups(M, quads, (long)grid.x * grid.y * grid.z);
@@ -1564,7 +1575,8 @@ void launch_qgemm_xs(const f16* x, int ldx, const uint8_t* wq, const uint16_t* w
   dim3 grid((NTILES + 4 * NT - 1) / (4 * NT), splits, (M + 16 * MT - 1) / (16 * MT));
   const int quads = (K / 128) / splits;
   auto go = [&]<int KG>() {
-    qgemm_xs_kernel<FMT, NT, MT, DW, 0, float, KG><<<grid, 256 * KG, 0, s>>>(x, ldx, wq, wd, part, M, N, K, quads);
+    qgemm_xs_kernel<FMT, NT, MT, xs_ring<FMT, MT, 0, KG, DW>, 0, float, KG>
+        <<<grid, 256 * KG, 0, s>>>(x, ldx, wq, wd, part, M, N, K, quads);
   };
   const int kg = xs_kgroups(M, quads, (long)grid.x * grid.y * grid.z);
   if constexpr (CIR_XS_KG >= 4) {

@@ -100,6 +100,63 @@ def test_default_splits_are_always_accepted():
     assert kernels.gemm_plan(hip.GEMM_PARTIALS, hip.CIR_Q8_0, 64, 2048, 11008, 15) != "invalid"
 
 
+def _llvm_tool(name: str):
+    for cand in (Path("/opt/rocm/llvm/bin") / name, shutil.which(name)):
+        if cand and Path(cand).exists():
+            return str(cand)
+    return None
+
+
+@pytest.mark.skipif(not hip.library_path().exists(), reason="libcacheir_hip.so not built")
+@pytest.mark.skipif(_llvm_tool("llvm-objcopy") is None or _llvm_tool("llvm-readelf") is None,
+                    reason="LLVM binutils not available")
+def test_no_kernel_spills_to_scratch(tmp_path):
+    """Every kernel in the built library keeps its values in registers: the gfx950 code objects' metadata gives a
+    private segment of 0 bytes for every kernel (a spill to scratch turns a register access into a memory round
+    trip and has cost 1.5x on a kernel here).  Reads the library's own device code: the .hip_fatbin section holds
+    one clang offload bundle per source file; each bundle's gfx950 entry is an ELF code object whose notes list
+    the kernels."""
+    import struct
+
+    fat = tmp_path / "fatbin.bin"
+    subprocess.run([_llvm_tool("llvm-objcopy"), f"--dump-section=.hip_fatbin={fat}", str(hip.library_path()),
+                    str(tmp_path / "lib_copy.so")], check=True, capture_output=True)
+    data = fat.read_bytes()
+    magic = b"__CLANG_OFFLOAD_BUNDLE__"
+    starts, i = [], data.find(magic)
+    while i >= 0:
+        starts.append(i)
+        i = data.find(magic, i + 1)
+    assert starts, "no offload bundle in .hip_fatbin"
+    kernels_seen, spills = 0, []
+    for b, start in enumerate(starts):
+        pos = start + len(magic)
+        (entries,) = struct.unpack_from("<Q", data, pos)
+        pos += 8
+        for _ in range(entries):
+            off, size, tlen = struct.unpack_from("<QQQ", data, pos)
+            pos += 24
+            triple = data[pos:pos + tlen].decode()
+            pos += tlen
+            if "gfx950" not in triple:
+                continue
+            obj = tmp_path / f"co{b}.o"
+            obj.write_bytes(data[start + off:start + off + size])
+            notes = subprocess.run([_llvm_tool("llvm-readelf"), "--notes", str(obj)], check=True,
+                                   capture_output=True, text=True).stdout
+            name = None
+            for line in notes.splitlines():
+                line = line.strip()
+                if line.startswith(".name:"):
+                    name = line.split(":", 1)[1].strip()
+                elif line.startswith(".private_segment_fixed_size:"):
+                    kernels_seen += 1
+                    if int(line.split(":", 1)[1]) != 0:
+                        spills.append((name, int(line.split(":", 1)[1])))
+    assert kernels_seen >= 100, f"only {kernels_seen} kernels found in the code objects"
+    assert not spills, spills[:10]
+
+
 def llama(layers=3, **kw):
     base = dict(architecture="LlamaForCausalLM", hidden_size=256, intermediate_size=512, num_layers=layers,
                 num_attention_heads=8, num_key_value_heads=2, vocab_size=1000, rope_theta=10000.0, rms_norm_eps=1e-5,

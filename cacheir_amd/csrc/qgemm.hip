@@ -642,7 +642,9 @@ __device__ __forceinline__ void buf16_to_lds(rsrc_t r, uint8_t* lds, uint32_t vo
 // gate/up tiles (one split), out[m][N/2] in type TO; EPI 2: greedy-head candidates
 // (one split), the best column of each wavefront's 32 and row: value in part, index in
 // act (as int), at [m][blockIdx.x * W + wave], for argmax_cand_kernel.
-template <int FMT, int MT, int DW, int EPI = 0, typename TO = float, int W = 4>
+// IL: ask the scheduler to interleave one MFMA with five VALU instructions (the block scale FMAs and dequant)
+// instead of its own two-MFMA / eight-FMA order; see launch_qgemm_xl for where that pays.
+template <int FMT, int MT, int DW, int EPI = 0, typename TO = float, int W = 4, bool IL = false>
 __global__ __launch_bounds__(64 * W) void qgemm_xl_kernel(const f16* __restrict__ x, int ldx,
                                                      const uint8_t* __restrict__ wq, const uint16_t* __restrict__ wd,
                                                      float* __restrict__ part, int M, int N, int K, int nq,
@@ -763,6 +765,13 @@ __global__ __launch_bounds__(64 * W) void qgemm_xl_kernel(const f16* __restrict_
 #pragma unroll
             for (int r = 0; r < 4; ++r) acc[a][b][r] = fmaf(dj[b][j], c[b][r], acc[a][b][r]);
         }
+      }
+    }
+    if constexpr (IL) {
+#pragma unroll
+      for (int i = 0; i < MT * 4 * NT; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);  // five VALU
       }
     }
   };
@@ -1654,8 +1663,17 @@ void launch_qgemm_xl(const f16* x, int ldx, const uint8_t* wq, const uint16_t* w
   constexpr int W = CIR_XL_W;
   const int NTILES = (N + 15) / 16;
   dim3 grid((NTILES + 2 * W - 1) / (2 * W), splits, (M + 16 * MT - 1) / (16 * MT));
-  qgemm_xl_kernel<FMT, MT, DW, EPI, TO, W>
-      <<<grid, 64 * W, 0, s>>>(x, ldx, wq, wd, part, M, N, K, (K / 128 + splits - 1) / splits, act);
+  const int nq = (K / 128 + splits - 1) / splits;
+  // Q8_0 partials in one round of workgroups (decode at m <= 128) take the interleave hint: at config 5 (m = 128)
+  // QKV 15.7 -> 14.6-14.8 us, down 41.7 -> 38.8-39.0.  Where the workgroups outnumber the CUs (prefill) its extra
+  // registers cost occupancy (Q8_0 m = 2048: QKV 120.3 -> 130.8 us), and Q4_0's lighter dequant gains nothing.
+  if constexpr (FMT == CIR_Q8_0 && EPI == 0) {
+    if ((long)grid.x * grid.y * grid.z <= kCUs) {
+      qgemm_xl_kernel<FMT, MT, DW, EPI, TO, W, true><<<grid, 64 * W, 0, s>>>(x, ldx, wq, wd, part, M, N, K, nq, act);
+      return;
+    }
+  }
+  qgemm_xl_kernel<FMT, MT, DW, EPI, TO, W><<<grid, 64 * W, 0, s>>>(x, ldx, wq, wd, part, M, N, K, nq, act);
 }
 
 // The fused greedy head on the large-m kernel (one split): 128 columns per workgroup, one

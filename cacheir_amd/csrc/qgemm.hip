@@ -643,8 +643,10 @@ __device__ __forceinline__ void buf16_to_lds(rsrc_t r, uint8_t* lds, uint32_t vo
 // (one split), the best column of each wavefront's 32 and row: value in part, index in
 // act (as int), at [m][blockIdx.x * W + wave], for argmax_cand_kernel.
 // IL: ask the scheduler to interleave one MFMA with five VALU instructions (the block scale FMAs and dequant)
-// instead of its own two-MFMA / eight-FMA order; see launch_qgemm_xl for where that pays.
-template <int FMT, int MT, int DW, int EPI = 0, typename TO = float, int W = 4, bool IL = false>
+// instead of its own two-MFMA / eight-FMA order; PF: convert each block scale to fp32 once and scale with plain
+// fp32 FMAs (the compiler otherwise reads the fp16 scale in every v_fma_mix_f32; same values, same bits).  See
+// launch_qgemm_xl for where each pays.
+template <int FMT, int MT, int DW, int EPI = 0, typename TO = float, int W = 4, bool IL = false, bool PF = false>
 __global__ __launch_bounds__(64 * W) void qgemm_xl_kernel(const f16* __restrict__ x, int ldx,
                                                      const uint8_t* __restrict__ wq, const uint16_t* __restrict__ wd,
                                                      float* __restrict__ part, int M, int N, int K, int nq,
@@ -740,6 +742,7 @@ __global__ __launch_bounds__(64 * W) void qgemm_xl_kernel(const f16* __restrict_
         if constexpr (!is_row_fmt(FMT)) {
           const uint32_t dw = (j < 2) ? st.d[b].x : st.d[b].y;
           dj[b][j] = static_cast<float>(__builtin_bit_cast(f16, (uint16_t)((j & 1) ? (dw >> 16) : (dw & 0xFFFFu))));
+          if constexpr (PF) asm volatile("" : "+v"(dj[b][j]));  // keeps the conversion out of the FMAs
         }
       }
     const uint8_t* xq = xslot ? smem1 : smem0;
@@ -1670,6 +1673,16 @@ void launch_qgemm_xl(const f16* x, int ldx, const uint8_t* wq, const uint16_t* w
   if constexpr (FMT == CIR_Q8_0 && EPI == 0) {
     if ((long)grid.x * grid.y * grid.z <= kCUs) {
       qgemm_xl_kernel<FMT, MT, DW, EPI, TO, W, true><<<grid, 64 * W, 0, s>>>(x, ldx, wq, wd, part, M, N, K, nq, act);
+      return;
+    }
+  }
+  // Launches of more workgroups than CUs (prefill sizes) convert the scales once (PF): at m = 2048 (Q4_0) gate|up +
+  // SwiGLU 568 -> 536 us, QKV 150 -> 142, O 98 -> 94, down 288 -> 282; a 2048-token prefill 43.7 -> 42.2 ms.
+  // Together with the interleave hint it measured slower (config 5's Q8_0 QKV 14.3 -> 16.2 us), and in the
+  // m <= 32 kernel and the GEMV too (batch-1 step 1.749 -> 1.771 ms).
+  if constexpr (!is_row_fmt(FMT)) {
+    if ((long)grid.x * grid.y * grid.z > kCUs) {
+      qgemm_xl_kernel<FMT, MT, DW, EPI, TO, W, false, true><<<grid, 64 * W, 0, s>>>(x, ldx, wq, wd, part, M, N, K, nq, act);
       return;
     }
   }

@@ -334,6 +334,38 @@ def test_qgemm_large_m_ragged_splits(device, fmt, m, n, k, splits):
     close16(part.sum(0), ops.matmul(x.astype(np.float32), wf.astype(np.float32)))
 
 
+@pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
+def test_qgemm_large_m_multi_round_matches_one_round(device, fmt):
+    """Launches of more workgroups than CUs (1100 rows: 36 column groups x 9 row blocks = 324 workgroups) take the
+    large-m kernel's plain-FMA scaling form; 512-row slices of the same inputs at one split (144 workgroups, one
+    round: the default form, for Q8_0 partials the interleave-hinted one) must give the same bits, for the partials
+    and for the fused SwiGLU.  At 4 splits both launches are multi-round: the slices check the row blocks (the last
+    one partly filled).  The partials' sum also within the fp16 bound of the oracle."""
+    from cacheir_amd import hip, kernels
+
+    rng = np.random.default_rng(1100 if fmt == "q4_0" else 1101)
+    enc, dec = (quant.random_q4_0, quant.decode_q4_0) if fmt == "q4_0" else (quant.random_q8_0, quant.decode_q8_0)
+    code = kernels.FMT_NAMES[fmt]
+    m, n, k = 1100, 4608, 1024
+    assert kernels.gemm_plan(hip.GEMM_PARTIALS, code, m, n, k, 1).startswith("qgemm_xl_kernel")
+    blocks = enc(rng, n, k)[0]
+    w = kernels.QWeight.from_blocks(to_dev(blocks.reshape(-1), device), code, n, k)
+    x = rng.standard_normal((m, k)).astype(np.float16)
+    xd = to_dev(x, device)
+    for splits in (1, 4):
+        got = kernels.qgemm_partial(xd, w, splits=splits)
+        for a in (0, 300, m - 512):
+            ref = kernels.qgemm_partial(xd[a:a + 512].contiguous(), w, splits=splits)
+            assert torch.equal(got[:, a:a + 512], ref), (splits, a)
+    close16(got.sum(0).cpu().numpy(), ops.matmul(x.astype(np.float32), dec(blocks, k).astype(np.float32)))
+    inter = n // 2
+    g_dev, u_dev = to_dev(enc(rng, inter, k)[0], device), to_dev(enc(rng, inter, k)[0], device)
+    w_il = kernels.QWeight.from_blocks(kernels.interleave_gate_up(g_dev, u_dev, inter).reshape(-1), code, n, k)
+    act = kernels.qgemm_swiglu(xd, w_il, torch.float16)
+    for a in (0, m - 512):
+        assert torch.equal(act[a:a + 512], kernels.qgemm_swiglu(xd[a:a + 512].contiguous(), w_il, torch.float16)), a
+
+
 @pytest.mark.parametrize("seed", range(12))
 def test_qgemm_planner_random_shapes(device, seed):
     """Seeded random shapes through the planner's own choices (``choose_splits``, then whichever kernel

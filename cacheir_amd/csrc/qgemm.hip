@@ -672,6 +672,10 @@ __global__ __launch_bounds__(64 * W) void qgemm_xl_kernel(const f16* __restrict_
                                                      TO* __restrict__ act = nullptr) {
   static_assert(EPI >= 0 && EPI <= 2, "large-m GEMM epilogues: partials, SwiGLU or argmax candidates");
   constexpr int NT = 2;
+  // Issue order of the block MFMAs and scale FMAs: pipelined by one block for the greedy head (Qwen2-7B lm_head
+  // at m = 128: 255.3-255.9 -> 245.6-246.2 us, alternated on one box); elsewhere it measured no better (2048-row
+  // gate|up + SwiGLU within noise) or worse (with the interleave hint: config 5's QKV 14.2 -> 15.1 us).
+  constexpr bool kPipe = !is_row_fmt(FMT) && EPI == 2;
   constexpr int LB = Stage<FMT, NT, 1>::LB;
   constexpr int kSlot = 16 * MT * 256;  // bytes of one quad of activations
   __shared__ __align__(16) uint8_t smem0[kSlot];  // two arrays, not one: the compiler then
@@ -777,7 +781,7 @@ __global__ __launch_bounds__(64 * W) void qgemm_xl_kernel(const f16* __restrict_
           for (int b = 0; b < NT; ++b) acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xf[j], wb[b][j], acc[a][b], 0, 0, 0);
           const f16x8 ones = {1, 1, 1, 1, 1, 1, 1, 1};
           sx[a] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xf[j], ones, sx[a], 0, 0, 0);
-        } else {
+        } else if constexpr (!kPipe) {
           f32x4 c[NT];
 #pragma unroll
           for (int b = 0; b < NT; ++b)
@@ -787,6 +791,28 @@ __global__ __launch_bounds__(64 * W) void qgemm_xl_kernel(const f16* __restrict_
 #pragma unroll
             for (int r = 0; r < 4; ++r) acc[a][b][r] = fmaf(dj[b][j], c[b][r], acc[a][b][r]);
         }
+      }
+      if constexpr (kPipe) {  // block j+1's MFMAs before block j's scale FMAs; same arithmetic and order
+        f32x4 c[2][NT];
+        auto mf = [&](int j, f32x4 (&cc)[NT]) __attribute__((always_inline)) {
+#pragma unroll
+          for (int b = 0; b < NT; ++b)
+            cc[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xf[j], wb[b][j], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+        };
+        auto fm = [&](int j, const f32x4 (&cc)[NT]) __attribute__((always_inline)) {
+#pragma unroll
+          for (int b = 0; b < NT; ++b)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[a][b][r] = fmaf(dj[b][j], cc[b][r], acc[a][b][r]);
+        };
+        mf(0, c[0]);
+        mf(1, c[1]);
+        fm(0, c[0]);
+        mf(2, c[0]);
+        fm(1, c[1]);
+        mf(3, c[1]);
+        fm(2, c[0]);
+        fm(3, c[1]);
       }
     }
     if constexpr (IL) {

@@ -276,7 +276,9 @@ struct Stage {
 // The MFMAs of block j + 1 are issued before the scale FMAs of block j (two sets of
 // block results in registers), so each FMA waits on an MFMA issued a block earlier:
 // config-4 step 3.452-3.463 -> 3.442-3.457 ms (three alternated pairs), batch 1 unchanged.
-template <int FMT, int NT, int MT>
+// MR: accumulator rows per lane group that are scaled (lane group g holds rows 4g .. 4g+3 of a
+// tile; at m = 1 only row 0 is real, and MR = 1 saves three of every four scale FMAs).
+template <int FMT, int NT, int MT, int MR = 4>
 __device__ __forceinline__ void compute_stage(const Stage<FMT, NT, MT>& st, f32x4 (&acc)[MT][NT]) {
   auto wfrag = [&](int b, int j) __attribute__((always_inline)) {
     f16x8 wb;
@@ -318,7 +320,7 @@ __device__ __forceinline__ void compute_stage(const Stage<FMT, NT, MT>& st, f32x
 #pragma unroll
         for (int a = 0; a < MT; ++a)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) acc[a][b][r] = fmaf(dj, cc[a][b][r], acc[a][b][r]);
+          for (int r = 0; r < MR; ++r) acc[a][b][r] = fmaf(dj, cc[a][b][r], acc[a][b][r]);
       }
     };
     mfmas(0, c[0]);
@@ -391,7 +393,7 @@ struct XsChunk {  // this thread's share of one quad of activations
 // EPI 2 (greedy head, one split): no logits are stored; each wavefront writes, per
 // row, the best (value, column) of its NT*16 columns to cand_v / cand_i
 // [m][wavefront] (part and act reinterpreted), reduced by argmax_cand_kernel.
-template <int FMT, int NT, int MT, int DW, int EPI = 0, typename TO = float, int KG = 1>
+template <int FMT, int NT, int MT, int DW, int EPI = 0, typename TO = float, int KG = 1, int MR = 4>
 __global__ __launch_bounds__(256 * KG) void qgemm_xs_kernel(const f16* __restrict__ x, int ldx,
                                                        const uint8_t* __restrict__ wq, const uint16_t* __restrict__ wd,
                                                        float* __restrict__ part, int M, int N, int K,
@@ -482,7 +484,7 @@ __global__ __launch_bounds__(256 * KG) void qgemm_xs_kernel(const f16* __restric
       for (int c = 0; c < LB; ++c) sg.w[b][c] = st.w[b][c];
       if constexpr (!is_row_fmt(FMT)) sg.d[b] = st.d[b];
     }
-    compute_stage(sg, acc);
+    compute_stage<FMT, NT, MT, MR>(sg, acc);
     if constexpr (is_row_fmt(FMT)) row_sums(sg.x, sx);
   };
 
@@ -1571,9 +1573,15 @@ void launch_qgemm_swiglu(const f16* x, int ldx, const uint8_t* wq, const uint16_
                          hipStream_t s) {
   const int NTILES = (N + 15) / 16;
   dim3 grid((NTILES + 7) / 8, 1, (M + 16 * MT - 1) / (16 * MT));
+  // One row (batch 1) scales only accumulator row 0 (MR = 1): gate|up + SwiGLU at the Llama-3-8B shape 16.9-17.7
+  // -> 16.1-16.6 us isolated, batch-1 step 1.741-1.743 -> 1.738-1.740 ms (three alternated pairs); the same bits.
   auto go = [&]<int KG>() {
-    qgemm_xs_kernel<FMT, 2, MT, xs_ring<FMT, MT, 1, KG, CIR_XS_DW_SWIGLU>, 1, TO, KG>
-        <<<grid, 256 * KG, 0, s>>>(x, ldx, wq, wd, nullptr, M, N, K, K / 128, act);
+    if (M == 1)
+      qgemm_xs_kernel<FMT, 2, MT, xs_ring<FMT, MT, 1, KG, CIR_XS_DW_SWIGLU>, 1, TO, KG, 1>
+          <<<grid, 256 * KG, 0, s>>>(x, ldx, wq, wd, nullptr, M, N, K, K / 128, act);
+    else
+      qgemm_xs_kernel<FMT, 2, MT, xs_ring<FMT, MT, 1, KG, CIR_XS_DW_SWIGLU>, 1, TO, KG>
+          <<<grid, 256 * KG, 0, s>>>(x, ldx, wq, wd, nullptr, M, N, K, K / 128, act);
   };
   const int kg = xs_kgroups(M, K / 128, (long)grid.x * grid.y * grid.z);
   if constexpr (CIR_XS_KG >= 4) {

@@ -182,6 +182,7 @@ class StepPlan:
         self._head: tuple | None = None  # (x, lm_head weight, workspace) when the greedy head can be fused
         self._head_at = 0
         self._gemm_need = 1
+        self._logits_swappable = False  # the logits GEMM writes ``self.logits`` as found at launch
         self._build(rt.artifact.graph(mode))
         self.gemm_ws = torch.empty(self._gemm_need, dtype=torch.float32, device=dev)
         attn_need = kernels.hip.size_call("cir_paged_attention_workspace_bytes", rows, rt.config.num_attention_heads,
@@ -357,10 +358,25 @@ class StepPlan:
                     self._head = (x16, W, kernels.qgemm_argmax_workspace(rows, W.n, rt.device))
                     rt._record_gemm_plan(hip.GEMM_ARGMAX, W, rows, 1)
                     env[ins[0]] = x16
-                part, _, n = gemm(env[ins[0]], W)
                 users = consumers.get(outs[0], [])
                 fuse = (len(users) == 1 and users[0].op == "add" and outs[0] in users[0].inputs
                         and outs[0] not in graph.outputs)
+                if (not fuse and isinstance(W, kernels.QWeight) and not isinstance(env[ins[0]], tuple)
+                        and kernels.choose_splits(rows, W.n, W.k) == 1):
+                    # one k-split: the GEMM's fp32 partial plane is the output itself (the store epilogue would
+                    # copy it bit for bit).  The logits GEMM writes whichever buffer ``self.logits`` holds at
+                    # launch, so an eager plan can hand its logits to the caller (``take_logits``).
+                    x = as_dtype(env[ins[0]], torch.float16)
+                    out = buf(W.n, torch.float32)
+                    is_logits = outs[0] == self.logits_name
+                    self.launches.append(lambda x=x, w=W, o=out, lg=is_logits: kernels.qgemm_partial(
+                        x, w, splits=1, out=self.logits if lg else o))
+                    self._logits_swappable |= is_logits
+                    rt._count("rocm.qgemm_blocks")
+                    rt._record_gemm_plan(hip.GEMM_PARTIALS, W, rows, 1)
+                    env[outs[0]] = out
+                    continue
+                part, _, n = gemm(env[ins[0]], W)
                 if fuse:
                     add = users[0]
                     other = add.inputs[1] if add.inputs[0] == outs[0] else add.inputs[0]
@@ -496,6 +512,16 @@ class StepPlan:
             fn()
         x, w, ws = self._head
         kernels.qgemm_argmax(x, w, out=self.next_ids, workspace=ws)
+
+    def take_logits(self) -> torch.Tensor:
+        """The logits of the step just launched, for the caller to keep.  A plan that has never been captured
+        and whose logits GEMM reads ``self.logits`` at launch hands that buffer over and writes its next step
+        into a fresh one (no copy); a captured plan writes a fixed address, so its logits are copied."""
+        if self.graph_obj is not None or self.graphs or not self._logits_swappable:
+            return self.logits.clone()
+        out = self.logits
+        self.logits = torch.empty(out.shape, dtype=out.dtype, device=out.device)
+        return out
 
     def capture(self, with_argmax: bool = True, greedy: bool = False) -> torch.cuda.CUDAGraph:
         """Capture the step into a HIP graph (after one eager warm-up on a side stream).  ``greedy`` captures
@@ -748,7 +774,7 @@ class HipRuntime:
     def _execute(self, caches: list[HipPagedKVCache], ids: np.ndarray, mode: str) -> torch.Tensor:
         batch, q_len = ids.shape
         plan = self._step(caches, ids, mode)
-        return plan.logits.view(batch, q_len, -1).clone()
+        return plan.take_logits().view(batch, q_len, -1)
 
     def run(self, input_ids, *, mode: str = "prefill", reset_kv: bool | None = None) -> torch.Tensor:
         """``cuda.py:508-539``: ``input_ids`` ``[S]`` or ``[B, S]`` -> logits ``[B, S, V]``.  A ``[B, S]`` batch is
@@ -853,7 +879,7 @@ class HipRuntime:
             self.kv_allocator.release([pad_slot])
         for c, n in zip(caches, lens):
             c.tokens += n
-        out = plan.logits.view(B, L, -1).clone()
+        out = plan.take_logits().view(B, L, -1)
         for b, n in enumerate(lens):
             if n < L:
                 out[b, n:] = 0

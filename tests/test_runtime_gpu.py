@@ -225,6 +225,43 @@ def test_block_quant_model_matches_oracle_and_gguf(tmp_path, device, fmt):
     assert np.array_equal(got2, got)
 
 
+@pytest.mark.parametrize("use_graphs", [False, True])
+def test_prefill_hands_its_logits_buffer_to_the_caller(tmp_path, device, use_graphs):
+    """A prefill whose LM head runs as one k-split writes the logits straight from the GEMM and returns the plan's
+    buffer itself (no store epilogue, no copy); the plan writes its next call into a fresh buffer, so an earlier
+    result is never overwritten, and the same prompt again gives the same bits.  Decode at batch 1 (two k-splits)
+    and captured decode plans copy their logits out, so those results stay the caller's too."""
+    from cacheir_amd import kernels
+    from cacheir_amd.runtime import HipRuntime
+
+    cfg, w, blocks, decoded = _q4_model(tmp_path, "q4_0")
+    art = compile_config(cfg, quant="q4_0", model_path=str(write_model(tmp_path / "m", cfg, w)))
+    rt = HipRuntime(art, use_graphs=use_graphs)
+    orc = OracleRuntime({m: g.to_dict() for m, g in art.graphs.items()}, decoded, cfg.vocab_size)
+    p1, p2 = list(range(5, 25)), list(range(30, 50))  # 20 tokens each: one plan
+    assert kernels.choose_splits(len(p1), cfg.vocab_size, cfg.hidden_size) == 1
+    a = rt.run([p1], mode="prefill")
+    a_host = a.cpu().numpy().copy()
+    close16(a_host, orc.run([p1], mode="prefill"))
+    plan = rt._plans[("prefill", 1, len(p1), rt._bucket(len(rt.kv_cache.slots)))]
+    assert plan._logits_swappable
+    fresh = plan.logits.data_ptr()
+    b = rt.run([p2], mode="prefill")
+    assert b.data_ptr() == fresh != a.data_ptr()
+    assert np.array_equal(a.cpu().numpy(), a_host)
+    close16(b.cpu().numpy(), orc.run([p2], mode="prefill"))
+    c = rt.run([p1], mode="prefill")
+    assert np.array_equal(c.cpu().numpy(), a_host)
+    orc.run([p1], mode="prefill")  # the oracle's cache now holds p1, as the runtime's does
+    d1 = rt.run([[7]], mode="decode")
+    d1_host = d1.cpu().numpy().copy()
+    close16(d1_host, orc.run([[7]], mode="decode"))
+    d2 = rt.run([[8]], mode="decode")
+    assert d2.data_ptr() != d1.data_ptr()
+    assert np.array_equal(d1.cpu().numpy(), d1_host)
+    close16(d2.cpu().numpy(), orc.run([[8]], mode="decode"))
+
+
 def test_graph_capture_replays_eager(tmp_path, device):
     from cacheir_amd.runtime import HipRuntime
 

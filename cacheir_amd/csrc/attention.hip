@@ -304,8 +304,9 @@ __global__ __launch_bounds__(64 * kWaves) void attn_f16_d128(
       if (hh <= G) {  // q or k: RoPE
         float sn, cs;
         sincosf((float)pos * fr[k], &sn, &cs);
-        // Rounded to fp32 before the fp16 conversion, as the QKV epilogue kernel does.
-        y = f16x2{static_cast<f16>(as_f32_value(x0 * cs - x1 * sn)), static_cast<f16>(as_f32_value(x0 * sn + x1 * cs))};
+        // The QKV epilogue kernel's operations: each FMA written out, rounded to fp32 before the fp16 conversion.
+        y = f16x2{static_cast<f16>(as_f32_value(fmaf(x0, cs, -(x1 * sn)))),
+                  static_cast<f16>(as_f32_value(fmaf(x0, sn, x1 * cs)))};
       } else {
         y = f16x2{static_cast<f16>(x0), static_cast<f16>(x1)};
       }

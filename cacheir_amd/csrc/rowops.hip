@@ -224,12 +224,6 @@ __global__ void cast_kernel(const TI* __restrict__ in, TO* __restrict__ out, siz
 }
 
 // ---------------------------------------------------------------- epilogues --
-__device__ __forceinline__ float split_sum(const float* __restrict__ part, int splits, size_t plane, size_t idx) {
-  float v = part[idx];
-  for (int s = 1; s < splits; ++s) v += part[(size_t)s * plane + idx];
-  return v;
-}
-
 // out = (residual +) sum of partials, 4 elements per thread (M*N % 4 == 0).
 template <int SMAX, typename T>
 __global__ void epi_store_kernel(const float* __restrict__ part, int splits, const T* __restrict__ resid,
@@ -268,52 +262,74 @@ __global__ void epi_swiglu_kernel(const float* __restrict__ part, int splits, T*
   out[i + 3] = from_f32<T>(silu_mul1(g.w, u.w));
 }
 
-// One thread per (row, rotation pair or v element).  Columns: q [Hq*D], k [Hkv*D], v [Hkv*D].
+// Sum of `splits` partial planes for the two columns idx, idx + 1 (idx even), added in split order as split_sum.
+__device__ __forceinline__ float2 split_sum2(const float* __restrict__ part, int splits, size_t plane, size_t idx) {
+  float2 v = *reinterpret_cast<const float2*>(part + idx);
+  for (int s = 1; s < splits; ++s) {
+    const float2 t = *reinterpret_cast<const float2*>(part + (size_t)s * plane + idx);
+    v.x += t.x;
+    v.y += t.y;
+  }
+  return v;
+}
+
+// Heads whose rotation pair i one thread rotates with one sincosf: at prompt positions in the thousands the
+// argument pos * inv_freq[i] takes the long range reduction, which cost more than the epilogue's memory traffic
+// when every (head, pair) evaluated it.
+constexpr int kRopeHeads = 8;
+
+// Columns: q [Hq*D], k [Hkv*D], v [Hkv*D], so q head h and k head h - Hq both start at column h*D.  Per row, one
+// thread per (group of kRopeHeads q/k heads, rotation pair i), then one per (v head, column pair).
 template <typename TQ, typename TK>
 __global__ void epi_qkv_kernel(const float* __restrict__ part, int splits, const float* __restrict__ inv_freq,
                                const int32_t* __restrict__ positions, const int32_t* __restrict__ pt, int max_pages,
                                TQ* __restrict__ q_out, TK* __restrict__ kp, TK* __restrict__ vp, int q_len, int Hq,
                                int Hkv, int D, int P, int rows) {
   const int half = D / 2;
-  const int q_pairs = Hq * half, k_pairs = Hkv * half, v_elems = Hkv * D;
-  const int per_row = q_pairs + k_pairs + v_elems;
+  const int H = Hq + Hkv;
+  const int rot = (H + kRopeHeads - 1) / kRopeHeads * half;
+  const int per_row = rot + Hkv * half;
   const long id = (long)blockIdx.x * blockDim.x + threadIdx.x;
   if (id >= (long)rows * per_row) return;
   const int r = (int)(id / per_row);
-  int c = (int)(id % per_row);
+  const int c = (int)(id % per_row);
   const int b = r / q_len, s = r % q_len;
   const int pos = positions[b] + s;
-  const int N = (Hq + 2 * Hkv) * D;
-  const size_t plane = (size_t)rows * N;
-  const float* base = part + (size_t)r * N;
-  auto col = [&](int j) { return split_sum(base, splits, plane, (size_t)j); };
+  const size_t plane = (size_t)rows * (H + Hkv) * D;
+  const float* base = part + (size_t)r * (H + Hkv) * D;
   const int page_idx = pos / P;
   const int slot = (page_idx < max_pages) ? pt[(size_t)b * max_pages + page_idx] : -1;
   const int off = pos - page_idx * P;
-  if (c < q_pairs + k_pairs) {
-    const bool is_q = c < q_pairs;
-    const int cc = is_q ? c : c - q_pairs;
-    const int head = cc / half, i = cc % half;
-    const int col0 = (is_q ? 0 : Hq * D) + head * D + 2 * i;
-    const float x0 = col(col0), x1 = col(col0 + 1);
+  if (c < rot) {
+    const int i = c % half, h0 = c / half * kRopeHeads;
     float sn, cs;
     sincosf((float)pos * inv_freq[i], &sn, &cs);
-    const float y0 = x0 * cs - x1 * sn;
-    const float y1 = x0 * sn + x1 * cs;
-    if (is_q) {
-      TQ* o = q_out + (size_t)r * Hq * D + head * D + 2 * i;
-      o[0] = from_f32<TQ>(y0);
-      o[1] = from_f32<TQ>(y1);
-    } else if (slot >= 0) {
-      TK* o = kp + (((size_t)slot * Hkv + head) * P + off) * D + 2 * i;
-      o[0] = from_f32<TK>(y0);
-      o[1] = from_f32<TK>(y1);
+#pragma unroll
+    for (int u = 0; u < kRopeHeads; ++u) {
+      const int h = h0 + u;
+      if (h >= H) break;
+      const float2 x = split_sum2(base, splits, plane, (size_t)h * D + 2 * i);
+      // The fused decode attention prologue rotates the same values with these same operations: each FMA written
+      // out (not left to contraction) and rounded to fp32 before an fp16 store (no single-rounding mixed FMA).
+      const float y0 = as_f32_value(fmaf(x.x, cs, -(x.y * sn)));
+      const float y1 = as_f32_value(fmaf(x.x, sn, x.y * cs));
+      if (h < Hq) {
+        TQ* o = q_out + ((size_t)r * Hq + h) * D + 2 * i;
+        o[0] = from_f32<TQ>(y0);
+        o[1] = from_f32<TQ>(y1);
+      } else if (slot >= 0) {
+        TK* o = kp + (((size_t)slot * Hkv + (h - Hq)) * P + off) * D + 2 * i;
+        o[0] = from_f32<TK>(y0);
+        o[1] = from_f32<TK>(y1);
+      }
     }
-  } else {
-    c -= q_pairs + k_pairs;
-    const int head = c / D, d = c % D;
-    const float v = col((Hq + Hkv) * D + head * D + d);
-    if (slot >= 0) vp[(((size_t)slot * Hkv + head) * P + off) * D + d] = from_f32<TK>(v);
+  } else if (slot >= 0) {
+    const int cc = c - rot;
+    const int head = cc / half, d = 2 * (cc % half);
+    const float2 v = split_sum2(base, splits, plane, (size_t)(H + head) * D + d);
+    TK* o = vp + (((size_t)slot * Hkv + head) * P + off) * D + d;
+    o[0] = from_f32<TK>(v.x);
+    o[1] = from_f32<TK>(v.y);
   }
 }
 
@@ -521,7 +537,8 @@ extern "C" int cir_epilogue_qkv_rope_append(const float* y_partial, int splits, 
   if (batch == 0) return 0;
   CIR_CHECK_ARG(y_partial && inv_freq && positions && page_table && q_out && k_pool && v_pool, "epilogue_qkv: null pointer");
   const int rows = batch * q_len;
-  const long total = (long)rows * (num_heads * (head_dim / 2) + num_kv_heads * (head_dim / 2) + num_kv_heads * head_dim);
+  const int rope_groups = (num_heads + num_kv_heads + kRopeHeads - 1) / kRopeHeads;
+  const long total = (long)rows * (rope_groups + num_kv_heads) * (head_dim / 2);
   hipStream_t s = as_stream(stream);
   const unsigned nb = (unsigned)((total + 255) / 256);
 #define CIR_QKV(TQ, TK)                                                                                            \

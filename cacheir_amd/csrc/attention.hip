@@ -587,6 +587,7 @@ constexpr int kPfKRow = 136;   // K row stride in LDS (halves): 256 B + 16, a ti
 constexpr int kPfVRow = 36;    // V^T row stride (halves): 64 B + 8; V is loaded 32 tokens x 2 column chunks per
                                // wavefront, so each transposed 2-byte write covers 32 banks
 
+template <bool PAIRED>
 __global__ __launch_bounds__(64 * kPfWaves) void attn_prefill_f16_d128(
     const f16* __restrict__ q, const f16* __restrict__ kp, const f16* __restrict__ vp,
     const int32_t* __restrict__ pt, const int32_t* __restrict__ lens, f16* __restrict__ out, int q_len, int Hq,
@@ -595,7 +596,7 @@ __global__ __launch_bounds__(64 * kPfWaves) void attn_prefill_f16_d128(
   static_assert(kBlock == 32 && 64 * kPfWaves == kBlock * (D / 8), "one 16-byte K and V chunk per thread");
   __shared__ __align__(16) f16 sk[2][kPfGroup][kBlock * kPfKRow];
   __shared__ __align__(16) f16 sv[2][kPfGroup][D * kPfVRow];
-  const int tile = gridDim.x - 1 - blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  const int kvh = blockIdx.y, b = blockIdx.z;
   const int G = Hq / Hkv;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int li = lane & 15, lg = lane >> 4;
@@ -607,152 +608,163 @@ __global__ __launch_bounds__(64 * kPfWaves) void attn_prefill_f16_d128(
   const int32_t* ptrow = pt + (size_t)b * max_pages;
   // Last key position query vector v sees (negative: none, its output is zero).
   auto pos_of = [&](int v) __attribute__((always_inline)) { return min(past + v / G, Lc - 1); };
-  const int tv0 = tile * 16 * kPfWaves;                     // the workgroup's first vector
-  const int tv1 = min(nvec, tv0 + 16 * kPfWaves) - 1;       // and its last
-  const int nblk = pos_of(tv1) >= 0 ? pos_of(tv1) / kBlock + 1 : 0;  // blocks the last token sees
-  const int v0 = tv0 + 16 * wave;                           // this wavefront's first vector
-  const int wlast = min(nvec - 1, v0 + 15);
-  const int wblk = (v0 < nvec && pos_of(wlast) >= 0) ? pos_of(wlast) / kBlock + 1 : 0;  // uniform
+  const int tiles = (nvec + 16 * kPfWaves - 1) / (16 * kPfWaves);
+  // Unpaired: one tile per workgroup, the last (longest) tiles first.  Paired: tile tiles - 1 - x, then tile x
+  // (once when they coincide), so every workgroup walks tiles + 1 tiles' worth of blocks under the causal mask.
+  for (int pass = 0; pass < (PAIRED ? 2 : 1); ++pass) {
+    const int tile = !PAIRED ? (int)(gridDim.x - 1 - blockIdx.x)
+                             : (pass == 0 ? tiles - 1 - (int)blockIdx.x : (int)blockIdx.x);
+    if (PAIRED && pass == 1) {
+      if (tile == tiles - 1 - (int)blockIdx.x) break;
+      __syncthreads();  // the first tile's LDS reads are done before the second's first stash
+    }
+    const int tv0 = tile * 16 * kPfWaves;                     // the workgroup's first vector
+    const int tv1 = min(nvec, tv0 + 16 * kPfWaves) - 1;       // and its last
+    const int nblk = pos_of(tv1) >= 0 ? pos_of(tv1) / kBlock + 1 : 0;  // blocks the last token sees
+    const int v0 = tv0 + 16 * wave;                           // this wavefront's first vector
+    const int wlast = min(nvec - 1, v0 + 15);
+    const int wblk = (v0 < nvec && pos_of(wlast) >= 0) ? pos_of(wlast) / kBlock + 1 : 0;  // uniform
 
-  // Thread t loads 16 bytes of K and of V per block: K at token t / 16, dims 8 * (t % 16); V at token t % 32,
-  // dims 8 * (t / 32).
-  const int lt = threadIdx.x >> 4, lc = threadIdx.x & 15;
-  const int vt = threadIdx.x & 31, vc = threadIdx.x >> 5;
-  f16x8 kr[kPfGroup], vr[kPfGroup];
-  auto load_group = [&](int g0, int nb) __attribute__((always_inline)) {
+    // Thread t loads 16 bytes of K and of V per block: K at token t / 16, dims 8 * (t % 16); V at token t % 32,
+    // dims 8 * (t / 32).
+    const int lt = threadIdx.x >> 4, lc = threadIdx.x & 15;
+    const int vt = threadIdx.x & 31, vc = threadIdx.x >> 5;
+    f16x8 kr[kPfGroup], vr[kPfGroup];
+    auto load_group = [&](int g0, int nb) __attribute__((always_inline)) {
 #pragma unroll
-    for (int i = 0; i < kPfGroup; ++i) {
-      if (i < nb) {
-        const int tok = min((g0 + i) * kBlock + lt, Lc - 1);  // past the context: masked, a valid page
-        const int page = ptrow[tok / P];
-        const size_t at = (((size_t)page * Hkv + kvh) * P + tok % P) * D + 8 * lc;
-        kr[i] = *reinterpret_cast<const f16x8*>(kp + at);
-        const int vtok = min((g0 + i) * kBlock + vt, Lc - 1);
-        const int vpage = ptrow[vtok / P];
-        vr[i] = *reinterpret_cast<const f16x8*>(vp + (((size_t)vpage * Hkv + kvh) * P + vtok % P) * D + 8 * vc);
+      for (int i = 0; i < kPfGroup; ++i) {
+        if (i < nb) {
+          const int tok = min((g0 + i) * kBlock + lt, Lc - 1);  // past the context: masked, a valid page
+          const int page = ptrow[tok / P];
+          const size_t at = (((size_t)page * Hkv + kvh) * P + tok % P) * D + 8 * lc;
+          kr[i] = *reinterpret_cast<const f16x8*>(kp + at);
+          const int vtok = min((g0 + i) * kBlock + vt, Lc - 1);
+          const int vpage = ptrow[vtok / P];
+          vr[i] = *reinterpret_cast<const f16x8*>(vp + (((size_t)vpage * Hkv + kvh) * P + vtok % P) * D + 8 * vc);
+        }
       }
-    }
-  };
-  auto stash_group = [&](int buf, int nb) __attribute__((always_inline)) {
+    };
+    auto stash_group = [&](int buf, int nb) __attribute__((always_inline)) {
 #pragma unroll
-    for (int i = 0; i < kPfGroup; ++i) {
-      if (i < nb) {
-        *reinterpret_cast<f16x8*>(&sk[buf][i][lt * kPfKRow + 8 * lc]) = kr[i];
+      for (int i = 0; i < kPfGroup; ++i) {
+        if (i < nb) {
+          *reinterpret_cast<f16x8*>(&sk[buf][i][lt * kPfKRow + 8 * lc]) = kr[i];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) sv[buf][i][(8 * vc + e) * kPfVRow + vt] = vr[i][e];
+          for (int e = 0; e < 8; ++e) sv[buf][i][(8 * vc + e) * kPfVRow + vt] = vr[i][e];
+        }
       }
-    }
-  };
-  if (nblk > 0) load_group(0, min(kPfGroup, nblk));
+    };
+    if (nblk > 0) load_group(0, min(kPfGroup, nblk));
 
-  // Q^T as the B operand (zero past the last vector), and each lane's query position.
-  f16x8 qb[4];
-  const int vq = v0 + li;
-  const bool live = vq < nvec;
-  const int qpos = pos_of(live ? vq : nvec - 1);
-  const int qmin = pos_of(min(v0, nvec - 1));  // the wavefront's first query position (the least)
-  {
-    const int vv = live ? vq : 0;
-    const int t = vv / G, g = vv - t * G;
-    const f16* qrow = q + (((size_t)b * q_len + t) * Hq + (size_t)kvh * G + g) * D + 8 * lg;
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const f16x8 x = *reinterpret_cast<const f16x8*>(qrow + 32 * s);
-      qb[s] = live ? x : f16x8{0, 0, 0, 0, 0, 0, 0, 0};
-    }
-  }
-  if (nblk > 0) stash_group(0, min(kPfGroup, nblk));
-  __syncthreads();
-
-  float m = -INFINITY, l = 0.f;  // query li: running max (every lane of the query), this lane's share of the sum
-  f32x4 acc[D / 16];             // O[query 4 lg + r][16 dt + li]
-#pragma unroll
-  for (int dt = 0; dt < D / 16; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  auto block = [&](int buf, int i, int blk) __attribute__((always_inline)) {
-    f32x4 c[kTiles];
-#pragma unroll
-    for (int j = 0; j < kTiles; ++j) {
-      c[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // Q^T as the B operand (zero past the last vector), and each lane's query position.
+    f16x8 qb[4];
+    const int vq = v0 + li;
+    const bool live = vq < nvec;
+    const int qpos = pos_of(live ? vq : nvec - 1);
+    const int qmin = pos_of(min(v0, nvec - 1));  // the wavefront's first query position (the least)
+    {
+      const int vv = live ? vq : 0;
+      const int t = vv / G, g = vv - t * G;
+      const f16* qrow = q + (((size_t)b * q_len + t) * Hq + (size_t)kvh * G + g) * D + 8 * lg;
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        const f16x8 a = *reinterpret_cast<const f16x8*>(&sk[buf][i][(16 * j + li) * kPfKRow + 32 * s + 8 * lg]);
-        c[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qb[s], c[j], 0, 0, 0);
+        const f16x8 x = *reinterpret_cast<const f16x8*>(qrow + 32 * s);
+        qb[s] = live ? x : f16x8{0, 0, 0, 0, 0, 0, 0, 0};
       }
     }
-    float mx = -INFINITY;
-    if (blk * kBlock + kBlock - 1 <= qmin) {  // uniform: every query of the wavefront sees the whole block
-#pragma unroll
-      for (int j = 0; j < kTiles; ++j)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          c[j][r] = c[j][r] * scale_log2;
-          mx = fmaxf(mx, c[j][r]);
-        }
-    } else {
-#pragma unroll
-      for (int j = 0; j < kTiles; ++j)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int key = blk * kBlock + 16 * j + 4 * lg + r;
-          c[j][r] = key <= qpos ? c[j][r] * scale_log2 : -INFINITY;
-          mx = fmaxf(mx, c[j][r]);
-        }
-    }
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    // Block 0 comes first and key 0 is visible to every query with a position, so m is finite from then on and
-    // a fully masked later block leaves mn = m, alpha = 1 and p = 0.  A query with no key at all keeps m = -inf:
-    // alpha 1 and p 0 (not the NaN of -inf - -inf), l stays 0 and its output 0.
-    const float mn = fmaxf(m, mx);
-    const bool none = mn == -INFINITY;
-    const float alpha = none ? 1.f : __builtin_amdgcn_exp2f(m - mn);
-    f16x8 pa;
-    float ps = 0.f;
-#pragma unroll
-    for (int j = 0; j < kTiles; ++j)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const f16 p = static_cast<f16>(none ? 0.f : __builtin_amdgcn_exp2f(c[j][r] - mn));
-        pa[4 * j + r] = p;
-        ps += static_cast<float>(p);
-      }
-    l = l * alpha + ps;
-    m = mn;
-    if (__builtin_amdgcn_ballot_w64(alpha != 1.f) != 0) {  // uniform
-#pragma unroll
-      for (int dt = 0; dt < D / 16; ++dt) acc[dt] *= alpha;
-    }
-#pragma unroll
-    for (int dt = 0; dt < D / 16; ++dt) {
-      const f16* vrow = &sv[buf][i][(16 * dt + li) * kPfVRow];
-      const f16x4 lo = *reinterpret_cast<const f16x4*>(vrow + 4 * lg);
-      const f16x4 hi = *reinterpret_cast<const f16x4*>(vrow + 16 + 4 * lg);
-      const f16x8 vb = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-      acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vb, pa, acc[dt], 0, 0, 0);
-    }
-  };
-  int buf = 0;
-  for (int g0 = 0; g0 < nblk; g0 += kPfGroup, buf ^= 1) {  // uniform
-    const int nb = min(kPfGroup, nblk - g0);
-    const int g1 = g0 + kPfGroup, nb1 = min(kPfGroup, nblk - g1);
-    if (nb1 > 0) load_group(g1, nb1);  // in flight during this group's math
-    for (int i = 0; i < nb; ++i)
-      if (g0 + i < wblk) block(buf, i, g0 + i);
-    if (nb1 > 0) stash_group(buf ^ 1, nb1);
+    if (nblk > 0) stash_group(0, min(kPfGroup, nblk));
     __syncthreads();
-  }
-  l += __shfl_xor(l, 16, 64);
-  l += __shfl_xor(l, 32, 64);
 
-  if (live) {
-    const int t = vq / G, g = vq - t * G;
-    f16* po = out + (((size_t)b * q_len + t) * Hq + (size_t)kvh * G + g) * D + 4 * lg;
-    const float inv = l > 0.f ? 1.f / l : 0.f;
+    float m = -INFINITY, l = 0.f;  // query li: running max (every lane of the query), this lane's share of the sum
+    f32x4 acc[D / 16];             // O[query 4 lg + r][16 dt + li]
 #pragma unroll
-    for (int dt = 0; dt < D / 16; ++dt)
-      *reinterpret_cast<f16x4*>(po + 16 * dt) = f16x4{static_cast<f16>(acc[dt][0] * inv), static_cast<f16>(acc[dt][1] * inv),
-                                                    static_cast<f16>(acc[dt][2] * inv), static_cast<f16>(acc[dt][3] * inv)};
-  }
+    for (int dt = 0; dt < D / 16; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    auto block = [&](int buf, int i, int blk) __attribute__((always_inline)) {
+      f32x4 c[kTiles];
+#pragma unroll
+      for (int j = 0; j < kTiles; ++j) {
+        c[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          const f16x8 a = *reinterpret_cast<const f16x8*>(&sk[buf][i][(16 * j + li) * kPfKRow + 32 * s + 8 * lg]);
+          c[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qb[s], c[j], 0, 0, 0);
+        }
+      }
+      float mx = -INFINITY;
+      if (blk * kBlock + kBlock - 1 <= qmin) {  // uniform: every query of the wavefront sees the whole block
+#pragma unroll
+        for (int j = 0; j < kTiles; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            c[j][r] = c[j][r] * scale_log2;
+            mx = fmaxf(mx, c[j][r]);
+          }
+      } else {
+#pragma unroll
+        for (int j = 0; j < kTiles; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int key = blk * kBlock + 16 * j + 4 * lg + r;
+            c[j][r] = key <= qpos ? c[j][r] * scale_log2 : -INFINITY;
+            mx = fmaxf(mx, c[j][r]);
+          }
+      }
+      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      // Block 0 comes first and key 0 is visible to every query with a position, so m is finite from then on and
+      // a fully masked later block leaves mn = m, alpha = 1 and p = 0.  A query with no key at all keeps m = -inf:
+      // alpha 1 and p 0 (not the NaN of -inf - -inf), l stays 0 and its output 0.
+      const float mn = fmaxf(m, mx);
+      const bool none = mn == -INFINITY;
+      const float alpha = none ? 1.f : __builtin_amdgcn_exp2f(m - mn);
+      f16x8 pa;
+      float ps = 0.f;
+#pragma unroll
+      for (int j = 0; j < kTiles; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const f16 p = static_cast<f16>(none ? 0.f : __builtin_amdgcn_exp2f(c[j][r] - mn));
+          pa[4 * j + r] = p;
+          ps += static_cast<float>(p);
+        }
+      l = l * alpha + ps;
+      m = mn;
+      if (__builtin_amdgcn_ballot_w64(alpha != 1.f) != 0) {  // uniform
+#pragma unroll
+        for (int dt = 0; dt < D / 16; ++dt) acc[dt] *= alpha;
+      }
+#pragma unroll
+      for (int dt = 0; dt < D / 16; ++dt) {
+        const f16* vrow = &sv[buf][i][(16 * dt + li) * kPfVRow];
+        const f16x4 lo = *reinterpret_cast<const f16x4*>(vrow + 4 * lg);
+        const f16x4 hi = *reinterpret_cast<const f16x4*>(vrow + 16 + 4 * lg);
+        const f16x8 vb = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vb, pa, acc[dt], 0, 0, 0);
+      }
+    };
+    int buf = 0;
+    for (int g0 = 0; g0 < nblk; g0 += kPfGroup, buf ^= 1) {  // uniform
+      const int nb = min(kPfGroup, nblk - g0);
+      const int g1 = g0 + kPfGroup, nb1 = min(kPfGroup, nblk - g1);
+      if (nb1 > 0) load_group(g1, nb1);  // in flight during this group's math
+      for (int i = 0; i < nb; ++i)
+        if (g0 + i < wblk) block(buf, i, g0 + i);
+      if (nb1 > 0) stash_group(buf ^ 1, nb1);
+      __syncthreads();
+    }
+    l += __shfl_xor(l, 16, 64);
+    l += __shfl_xor(l, 32, 64);
+
+    if (live) {
+      const int t = vq / G, g = vq - t * G;
+      f16* po = out + (((size_t)b * q_len + t) * Hq + (size_t)kvh * G + g) * D + 4 * lg;
+      const float inv = l > 0.f ? 1.f / l : 0.f;
+#pragma unroll
+      for (int dt = 0; dt < D / 16; ++dt)
+        *reinterpret_cast<f16x4*>(po + 16 * dt) = f16x4{static_cast<f16>(acc[dt][0] * inv), static_cast<f16>(acc[dt][1] * inv),
+                                                      static_cast<f16>(acc[dt][2] * inv), static_cast<f16>(acc[dt][3] * inv)};
+    }
+  }  // pass
 }
 
 // ----------------------------------------------------------------------------
@@ -965,7 +977,11 @@ int launch_attention(const void* q, const void* k_pool, const void* v_pool, cons
   dim3 grid(S, Hkv, rows);
   if (mfma && q_len > 1) {  // prefill: query tiles of 128 vectors over each sequence's blocks, no partials
     const int tiles = (q_len * G + 16 * kPfWaves - 1) / (16 * kPfWaves);
-    attn_prefill_f16_d128<<<dim3(tiles, Hkv, batch), 64 * kPfWaves, 0, s>>>(
+    // Pairs of tiles per workgroup once the unpaired grid fills every CU's two workgroup slots: the causal
+    // mask's long and short tiles then share a workgroup instead of the longest setting the kernel's time.
+    const bool paired = tiles > 1 && (long)tiles * Hkv * batch >= 2L * device_cus();
+    const auto kernel = paired ? attn_prefill_f16_d128<true> : attn_prefill_f16_d128<false>;
+    kernel<<<dim3(paired ? (tiles + 1) / 2 : tiles, Hkv, batch), 64 * kPfWaves, 0, s>>>(
         static_cast<const f16*>(q), static_cast<const f16*>(k_pool), static_cast<const f16*>(v_pool), page_table,
         seq_lens, static_cast<f16*>(out), q_len, Hq, Hkv, P, max_pages, scale_log2);
     return launch_status();

@@ -201,6 +201,40 @@ def test_prefill_attention_fp16_random_shapes(device, seed):
         close16(out[b * q_len:(b + 1) * q_len], ref)
 
 
+@pytest.mark.parametrize("q_len", [600, 590])
+def test_prefill_attention_paired_tiles(device, q_len):
+    """A prefill grid of at least two workgroups per CU runs tile pairs (tiles - 1 - x, then x) in one workgroup:
+    an even and an odd tile count (600 / 590 tokens x 8 query heads over 1 KV head: 38 / 37 tiles of 128 query
+    vectors, the odd one with a middle tile run once), 14 sequences after 0-300 tokens of context.  The batch
+    agrees with the oracle, and bit for bit with each sequence launched alone (38 workgroups: unpaired)."""
+    from cacheir_amd import kernels
+
+    rng = np.random.default_rng(q_len)
+    batch, hkv, g = 14, 1, 8
+    hq = g * hkv
+    tiles = -(-q_len * g // 128)
+    assert tiles * hkv * batch >= 2 * torch.cuda.get_device_properties(0).multi_processor_count
+    past = rng.integers(0, 301, batch)
+    total = past + q_len
+    kp, vp, pt, lens = paged.build_pool(rng, total, hkv, 128, 16)
+    q = rng.standard_normal((batch * q_len, hq, 128)).astype(np.float16)
+    kpd, vpd, ptd = to_dev(kp, device), to_dev(vp, device), to_dev(pt, device)
+    out = kernels.paged_prefill_attention(to_dev(q, device), kpd, vpd, ptd, to_dev(lens, device), q_len,
+                                          check_tables=True)
+    for b in range(batch):
+        alone = kernels.paged_prefill_attention(to_dev(q[b * q_len:(b + 1) * q_len], device), kpd, vpd,
+                                                ptd[b:b + 1].contiguous(), to_dev(lens[b:b + 1], device), q_len,
+                                                check_tables=True)
+        assert torch.equal(alone, out[b * q_len:(b + 1) * q_len]), f"sequence {b}"
+    out = out.float().cpu().numpy()
+    for b in range(batch):
+        kh = paged.gather_sequence(kp, pt[b], int(total[b])).astype(np.float32)[None]
+        vh = paged.gather_sequence(vp, pt[b], int(total[b])).astype(np.float32)[None]
+        qh = q[b * q_len:(b + 1) * q_len].astype(np.float32)[None]
+        ref = ops.attention(qh, kh, vh, hq, hkv, 128, causal=True).reshape(q_len, hq, 128)
+        close16(out[b * q_len:(b + 1) * q_len], ref)
+
+
 # -------------------------------------------------------------- block weights --
 @pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
 def test_dequant_bit_exact(device, fmt):

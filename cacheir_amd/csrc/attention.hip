@@ -581,6 +581,12 @@ __global__ __launch_bounds__(64 * kWaves) void attn_f16_d128(
 // CU.  Against one workgroup per CU at four blocks per buffer (140 KiB), the library
 // exp2f, O = P V and V^T written 4 tokens x 16 column chunks per wavefront (4 banks), a
 // 2048-token prompt (32/8 heads) took 135 against 224 us, 4 x 512 tokens 44 against 66.
+// PAIRED: once the one-tile grid fills both workgroup slots of every CU, all of it is
+// resident at once and the longest tiles set the kernel's time (at 2048 tokens tile 63
+// walks 64 blocks, the mean is 32.5).  A workgroup then runs tile tiles - 1 - x and tile
+// x one after the other (tiles + 1 tiles' worth of blocks each, one workgroup per CU,
+// 120 VGPRs): 2048 tokens 121 us, 4096 tokens 308 against 401, 8 x 512 tokens 60 against
+// 80, the same bits.  Smaller grids keep one tile per workgroup.
 constexpr int kPfWaves = 8;
 constexpr int kPfGroup = 2;    // blocks per LDS buffer (two buffers: 70 KiB)
 constexpr int kPfKRow = 136;   // K row stride in LDS (halves): 256 B + 16, a tile's rows on distinct banks

@@ -593,15 +593,16 @@ constexpr int kPfKRow = 136;   // K row stride in LDS (halves): 256 B + 16, a ti
 constexpr int kPfVRow = 36;    // V^T row stride (halves): 64 B + 8; V is loaded 32 tokens x 2 column chunks per
                                // wavefront, so each transposed 2-byte write covers 32 banks
 
-template <bool PAIRED>
+template <bool PAIRED, int NG>
 __global__ __launch_bounds__(64 * kPfWaves) void attn_prefill_f16_d128(
     const f16* __restrict__ q, const f16* __restrict__ kp, const f16* __restrict__ vp,
     const int32_t* __restrict__ pt, const int32_t* __restrict__ lens, f16* __restrict__ out, int q_len, int Hq,
     int Hkv, int P, int max_pages, float scale_log2) {
   constexpr int D = 128;
   static_assert(kBlock == 32 && 64 * kPfWaves == kBlock * (D / 8), "one 16-byte K and V chunk per thread");
-  __shared__ __align__(16) f16 sk[2][kPfGroup][kBlock * kPfKRow];
-  __shared__ __align__(16) f16 sv[2][kPfGroup][D * kPfVRow];
+  static_assert(NG == kPfGroup || (PAIRED && NG == 2 * kPfGroup), "blocks per LDS buffer");
+  __shared__ __align__(16) f16 sk[2][NG][kBlock * kPfKRow];
+  __shared__ __align__(16) f16 sv[2][NG][D * kPfVRow];
   const int kvh = blockIdx.y, b = blockIdx.z;
   const int G = Hq / Hkv;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
@@ -635,10 +636,10 @@ __global__ __launch_bounds__(64 * kPfWaves) void attn_prefill_f16_d128(
     // dims 8 * (t / 32).
     const int lt = threadIdx.x >> 4, lc = threadIdx.x & 15;
     const int vt = threadIdx.x & 31, vc = threadIdx.x >> 5;
-    f16x8 kr[kPfGroup], vr[kPfGroup];
+    f16x8 kr[NG], vr[NG];
     auto load_group = [&](int g0, int nb) __attribute__((always_inline)) {
 #pragma unroll
-      for (int i = 0; i < kPfGroup; ++i) {
+      for (int i = 0; i < NG; ++i) {
         if (i < nb) {
           const int tok = min((g0 + i) * kBlock + lt, Lc - 1);  // past the context: masked, a valid page
           const int page = ptrow[tok / P];
@@ -652,7 +653,7 @@ __global__ __launch_bounds__(64 * kPfWaves) void attn_prefill_f16_d128(
     };
     auto stash_group = [&](int buf, int nb) __attribute__((always_inline)) {
 #pragma unroll
-      for (int i = 0; i < kPfGroup; ++i) {
+      for (int i = 0; i < NG; ++i) {
         if (i < nb) {
           *reinterpret_cast<f16x8*>(&sk[buf][i][lt * kPfKRow + 8 * lc]) = kr[i];
 #pragma unroll
@@ -660,7 +661,7 @@ __global__ __launch_bounds__(64 * kPfWaves) void attn_prefill_f16_d128(
         }
       }
     };
-    if (nblk > 0) load_group(0, min(kPfGroup, nblk));
+    if (nblk > 0) load_group(0, min(NG, nblk));
 
     // Q^T as the B operand (zero past the last vector), and each lane's query position.
     f16x8 qb[4];
@@ -678,7 +679,7 @@ __global__ __launch_bounds__(64 * kPfWaves) void attn_prefill_f16_d128(
         qb[s] = live ? x : f16x8{0, 0, 0, 0, 0, 0, 0, 0};
       }
     }
-    if (nblk > 0) stash_group(0, min(kPfGroup, nblk));
+    if (nblk > 0) stash_group(0, min(NG, nblk));
     __syncthreads();
 
     float m = -INFINITY, l = 0.f;  // query li: running max (every lane of the query), this lane's share of the sum
@@ -749,9 +750,9 @@ __global__ __launch_bounds__(64 * kPfWaves) void attn_prefill_f16_d128(
       }
     };
     int buf = 0;
-    for (int g0 = 0; g0 < nblk; g0 += kPfGroup, buf ^= 1) {  // uniform
-      const int nb = min(kPfGroup, nblk - g0);
-      const int g1 = g0 + kPfGroup, nb1 = min(kPfGroup, nblk - g1);
+    for (int g0 = 0; g0 < nblk; g0 += NG, buf ^= 1) {  // uniform
+      const int nb = min(NG, nblk - g0);
+      const int g1 = g0 + NG, nb1 = min(NG, nblk - g1);
       if (nb1 > 0) load_group(g1, nb1);  // in flight during this group's math
       for (int i = 0; i < nb; ++i)
         if (g0 + i < wblk) block(buf, i, g0 + i);
@@ -986,7 +987,12 @@ int launch_attention(const void* q, const void* k_pool, const void* v_pool, cons
     // Pairs of tiles per workgroup once the unpaired grid fills every CU's two workgroup slots: the causal
     // mask's long and short tiles then share a workgroup instead of the longest setting the kernel's time.
     const bool paired = tiles > 1 && (long)tiles * Hkv * batch >= 2L * device_cus();
-    const auto kernel = paired ? attn_prefill_f16_d128<true> : attn_prefill_f16_d128<false>;
+    // A paired grid of at most one workgroup per CU stages twice the blocks per buffer (143 KiB of LDS, twice the
+    // loads in flight); a larger one keeps 70 KiB so two workgroups share a CU and the grid runs in one round.
+    const bool deep = paired && (long)((tiles + 1) / 2) * Hkv * batch <= device_cus();
+    const auto kernel = !paired ? attn_prefill_f16_d128<false, kPfGroup>
+                        : deep  ? attn_prefill_f16_d128<true, 2 * kPfGroup>
+                                : attn_prefill_f16_d128<true, kPfGroup>;
     kernel<<<dim3(paired ? (tiles + 1) / 2 : tiles, Hkv, batch), 64 * kPfWaves, 0, s>>>(
         static_cast<const f16*>(q), static_cast<const f16*>(k_pool), static_cast<const f16*>(v_pool), page_table,
         seq_lens, static_cast<f16*>(out), q_len, Hq, Hkv, P, max_pages, scale_log2);

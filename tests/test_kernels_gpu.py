@@ -201,19 +201,22 @@ def test_prefill_attention_fp16_random_shapes(device, seed):
         close16(out[b * q_len:(b + 1) * q_len], ref)
 
 
-@pytest.mark.parametrize("q_len", [600, 590])
-def test_prefill_attention_paired_tiles(device, q_len):
+@pytest.mark.parametrize("q_len,batch", [(600, 14), (590, 14), (512, 16)])
+def test_prefill_attention_paired_tiles(device, q_len, batch):
     """A prefill grid of at least two workgroups per CU runs tile pairs (tiles - 1 - x, then x) in one workgroup:
     an even and an odd tile count (600 / 590 tokens x 8 query heads over 1 KV head: 38 / 37 tiles of 128 query
-    vectors, the odd one with a middle tile run once), 14 sequences after 0-300 tokens of context.  The batch
-    agrees with the oracle, and bit for bit with each sequence launched alone (38 workgroups: unpaired)."""
+    vectors, the odd one with a middle tile run once; 266 paired workgroups, 2 K/V blocks per LDS buffer), and 16
+    sequences of 32 tiles (256 paired workgroups, at most one per CU: 4 blocks per buffer), after 0-300 tokens of
+    context.  The batch agrees with the oracle, and bit for bit with each sequence launched alone (unpaired)."""
     from cacheir_amd import kernels
 
     rng = np.random.default_rng(q_len)
-    batch, hkv, g = 14, 1, 8
+    hkv, g = 1, 8
     hq = g * hkv
     tiles = -(-q_len * g // 128)
-    assert tiles * hkv * batch >= 2 * torch.cuda.get_device_properties(0).multi_processor_count
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    assert tiles * hkv * batch >= 2 * cus
+    assert ((tiles + 1) // 2 * hkv * batch <= cus) == (q_len == 512)
     past = rng.integers(0, 301, batch)
     total = past + q_len
     kp, vp, pt, lens = paged.build_pool(rng, total, hkv, 128, 16)

@@ -584,9 +584,12 @@ __global__ __launch_bounds__(64 * kWaves) void attn_f16_d128(
 // PAIRED: once the one-tile grid fills both workgroup slots of every CU, all of it is
 // resident at once and the longest tiles set the kernel's time (at 2048 tokens tile 63
 // walks 64 blocks, the mean is 32.5).  A workgroup then runs tile tiles - 1 - x and tile
-// x one after the other (tiles + 1 tiles' worth of blocks each, one workgroup per CU,
-// 120 VGPRs): 2048 tokens 121 us, 4096 tokens 308 against 401, 8 x 512 tokens 60 against
-// 80, the same bits.  Smaller grids keep one tile per workgroup.
+// x one after the other (tiles + 1 tiles' worth of blocks each, 120 VGPRs): 2048 tokens
+// 121 us, 4096 tokens 308 against 401, 8 x 512 tokens 60 against 80, the same bits.
+// Smaller grids keep one tile per workgroup.  NG: blocks per LDS buffer.  A paired grid
+// of at most one workgroup per CU takes 4 (143 KiB, 166 VGPRs), twice the loads in
+// flight: 2048 tokens 110 us, 2 x 1024 61 against 67; a larger one would then run in
+// two rounds (4096 tokens 374 against 289), so it keeps 2.
 constexpr int kPfWaves = 8;
 constexpr int kPfGroup = 2;    // blocks per LDS buffer (two buffers: 70 KiB)
 constexpr int kPfKRow = 136;   // K row stride in LDS (halves): 256 B + 16, a tile's rows on distinct banks

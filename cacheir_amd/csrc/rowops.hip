@@ -289,11 +289,12 @@ __global__ void epi_qkv_kernel(const float* __restrict__ part, int splits, const
   const int H = Hq + Hkv;
   const int rot = (H + kRopeHeads - 1) / kRopeHeads * half;
   const int per_row = rot + Hkv * half;
-  const long id = (long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (id >= (long)rows * per_row) return;
-  const int r = (int)(id / per_row);
-  const int c = (int)(id % per_row);
-  const int b = r / q_len, s = r % q_len;
+  // 32-bit unsigned index arithmetic (the launcher keeps rows * per_row below 2^31)
+  const unsigned id = blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= (unsigned)(rows * per_row)) return;
+  const int r = (int)(id / (unsigned)per_row);
+  const int c = (int)(id % (unsigned)per_row);
+  const int b = (int)((unsigned)r / (unsigned)q_len), s = r - b * q_len;
   const int pos = positions[b] + s;
   const size_t plane = (size_t)rows * (H + Hkv) * D;
   const float* base = part + (size_t)r * (H + Hkv) * D;
@@ -301,7 +302,7 @@ __global__ void epi_qkv_kernel(const float* __restrict__ part, int splits, const
   const int slot = (page_idx < max_pages) ? pt[(size_t)b * max_pages + page_idx] : -1;
   const int off = pos - page_idx * P;
   if (c < rot) {
-    const int i = c % half, h0 = c / half * kRopeHeads;
+    const int hq = (int)((unsigned)c / (unsigned)half), i = c - hq * half, h0 = hq * kRopeHeads;
     float sn, cs;
     sincosf((float)pos * inv_freq[i], &sn, &cs);
 #pragma unroll
@@ -325,7 +326,7 @@ __global__ void epi_qkv_kernel(const float* __restrict__ part, int splits, const
     }
   } else if (slot >= 0) {
     const int cc = c - rot;
-    const int head = cc / half, d = 2 * (cc % half);
+    const int head = (int)((unsigned)cc / (unsigned)half), d = 2 * (cc - head * half);
     const float2 v = split_sum2(base, splits, plane, (size_t)(H + head) * D + d);
     TK* o = vp + (((size_t)slot * Hkv + head) * P + off) * D + d;
     o[0] = from_f32<TK>(v.x);
@@ -539,6 +540,7 @@ extern "C" int cir_epilogue_qkv_rope_append(const float* y_partial, int splits, 
   const int rows = batch * q_len;
   const int rope_groups = (num_heads + num_kv_heads + kRopeHeads - 1) / kRopeHeads;
   const long total = (long)rows * (rope_groups + num_kv_heads) * (head_dim / 2);
+  CIR_CHECK_ARG(total < (1L << 31), "epilogue_qkv: %ld work items exceed the kernel's 32-bit index", total);
   hipStream_t s = as_stream(stream);
   const unsigned nb = (unsigned)((total + 255) / 256);
 #define CIR_QKV(TQ, TK)                                                                                            \

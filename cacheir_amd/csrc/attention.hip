@@ -586,10 +586,10 @@ __global__ __launch_bounds__(64 * kWaves) void attn_f16_d128(
 // walks 64 blocks, the mean is 32.5).  A workgroup then runs tile tiles - 1 - x and tile
 // x one after the other (tiles + 1 tiles' worth of blocks each, 120 VGPRs): 2048 tokens
 // 121 us, 4096 tokens 308 against 401, 8 x 512 tokens 60 against 80, the same bits.
-// Smaller grids keep one tile per workgroup.  NG: blocks per LDS buffer.  A paired grid
-// of at most one workgroup per CU takes 4 (143 KiB, 166 VGPRs), twice the loads in
-// flight: 2048 tokens 110 us, 2 x 1024 61 against 67; a larger one would then run in
-// two rounds (4096 tokens 374 against 289), so it keeps 2.
+// Smaller grids keep one tile per workgroup.  NG: blocks per LDS buffer.  A grid of at
+// most one workgroup per CU takes 4 (143 KiB; 166 VGPRs paired, 129 not), twice the loads
+// in flight: 2048 tokens 110 us, 2 x 1024 61 against 67, 2 x 512 28.1 against 29.2; a
+// larger one would then run in two rounds (4096 tokens 374 against 289), so it keeps 2.
 constexpr int kPfWaves = 8;
 constexpr int kPfGroup = 2;    // blocks per LDS buffer (two buffers: 70 KiB)
 constexpr int kPfKRow = 136;   // K row stride in LDS (halves): 256 B + 16, a tile's rows on distinct banks
@@ -603,7 +603,7 @@ __global__ __launch_bounds__(64 * kPfWaves) void attn_prefill_f16_d128(
     int Hkv, int P, int max_pages, float scale_log2) {
   constexpr int D = 128;
   static_assert(kBlock == 32 && 64 * kPfWaves == kBlock * (D / 8), "one 16-byte K and V chunk per thread");
-  static_assert(NG == kPfGroup || (PAIRED && NG == 2 * kPfGroup), "blocks per LDS buffer");
+  static_assert(NG == kPfGroup || NG == 2 * kPfGroup, "blocks per LDS buffer");
   __shared__ __align__(16) f16 sk[2][NG][kBlock * kPfKRow];
   __shared__ __align__(16) f16 sv[2][NG][D * kPfVRow];
   const int kvh = blockIdx.y, b = blockIdx.z;
@@ -989,13 +989,15 @@ int launch_attention(const void* q, const void* k_pool, const void* v_pool, cons
     const int tiles = (q_len * G + 16 * kPfWaves - 1) / (16 * kPfWaves);
     // Pairs of tiles per workgroup once the unpaired grid fills every CU's two workgroup slots: the causal
     // mask's long and short tiles then share a workgroup instead of the longest setting the kernel's time.
-    const bool paired = tiles > 1 && (long)tiles * Hkv * batch >= 2L * device_cus();
-    // A paired grid of at most one workgroup per CU stages twice the blocks per buffer (143 KiB of LDS, twice the
-    // loads in flight); a larger one keeps 70 KiB so two workgroups share a CU and the grid runs in one round.
-    const bool deep = paired && (long)((tiles + 1) / 2) * Hkv * batch <= device_cus();
-    const auto kernel = !paired ? attn_prefill_f16_d128<false, kPfGroup>
-                        : deep  ? attn_prefill_f16_d128<true, 2 * kPfGroup>
-                                : attn_prefill_f16_d128<true, kPfGroup>;
+    const long one_tile = (long)tiles * Hkv * batch;
+    const bool paired = tiles > 1 && one_tile >= 2L * device_cus();
+    const long workgroups = paired ? (long)((tiles + 1) / 2) * Hkv * batch : one_tile;
+    // A grid of at most one workgroup per CU stages twice the blocks per buffer (143 KiB of LDS, twice the loads
+    // in flight); a larger one keeps 70 KiB so two workgroups share a CU and the grid runs in one round.
+    const bool deep = workgroups <= device_cus();
+    const auto kernel = paired ? (deep ? attn_prefill_f16_d128<true, 2 * kPfGroup> : attn_prefill_f16_d128<true, kPfGroup>)
+                               : (deep ? attn_prefill_f16_d128<false, 2 * kPfGroup>
+                                       : attn_prefill_f16_d128<false, kPfGroup>);
     kernel<<<dim3(paired ? (tiles + 1) / 2 : tiles, Hkv, batch), 64 * kPfWaves, 0, s>>>(
         static_cast<const f16*>(q), static_cast<const f16*>(k_pool), static_cast<const f16*>(v_pool), page_table,
         seq_lens, static_cast<f16*>(out), q_len, Hq, Hkv, P, max_pages, scale_log2);

@@ -201,13 +201,15 @@ def test_prefill_attention_fp16_random_shapes(device, seed):
         close16(out[b * q_len:(b + 1) * q_len], ref)
 
 
-@pytest.mark.parametrize("q_len,batch", [(600, 14), (590, 14), (512, 16)])
+@pytest.mark.parametrize("q_len,batch", [(600, 14), (590, 14), (512, 16), (600, 10)])
 def test_prefill_attention_paired_tiles(device, q_len, batch):
     """A prefill grid of at least two workgroups per CU runs tile pairs (tiles - 1 - x, then x) in one workgroup:
     an even and an odd tile count (600 / 590 tokens x 8 query heads over 1 KV head: 38 / 37 tiles of 128 query
     vectors, the odd one with a middle tile run once; 266 paired workgroups, 2 K/V blocks per LDS buffer), and 16
     sequences of 32 tiles (256 paired workgroups, at most one per CU: 4 blocks per buffer), after 0-300 tokens of
-    context.  The batch agrees with the oracle, and bit for bit with each sequence launched alone (unpaired)."""
+    context.  The batch agrees with the oracle, and bit for bit with each sequence launched alone (unpaired, one
+    workgroup per CU at most: 4 blocks per buffer).  10 sequences of 38 tiles (380 workgroups) run unpaired with
+    2 blocks per buffer, against the same checks."""
     from cacheir_amd import kernels
 
     rng = np.random.default_rng(q_len)
@@ -215,8 +217,11 @@ def test_prefill_attention_paired_tiles(device, q_len, batch):
     hq = g * hkv
     tiles = -(-q_len * g // 128)
     cus = torch.cuda.get_device_properties(0).multi_processor_count
-    assert tiles * hkv * batch >= 2 * cus
-    assert ((tiles + 1) // 2 * hkv * batch <= cus) == (q_len == 512)
+    one_tile = tiles * hkv * batch
+    paired = one_tile >= 2 * cus
+    assert paired == (batch != 10)
+    workgroups = (tiles + 1) // 2 * hkv * batch if paired else one_tile
+    assert (workgroups <= cus) == (q_len == 512)  # 4 K/V blocks per LDS buffer
     past = rng.integers(0, 301, batch)
     total = past + q_len
     kp, vp, pt, lens = paged.build_pool(rng, total, hkv, 128, 16)
